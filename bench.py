@@ -1,0 +1,287 @@
+#!/usr/bin/env python3
+"""Benchmark of the INT8 KV-cache path on one MI355X.
+
+Metric: "30K-prefill INT8-KV attn ms/layer (MFMA %); 128K decode KV-read GB/s".
+
+* step (``value``, ms per layer): config 3 — a 30720-token causal prompt of one
+  full-attention layer in 60 chunks of 512 tokens. Per chunk, exactly the engine's
+  INT8 sequence (Prefill.cs:255-261): batch_rope_int8 (rotate Q, rotate K, INT8 append)
+  -> attention_query_grouped_half -> attention_online_int8 (+ split combine).
+  Inputs (FP32 Q/K/V, gate) are resident in HBM before timing; synthetic N(0,1) with
+  K channels {30,31,62,63} x 20; 16 Q / 2 KV heads, d = 256.
+* decode (extra keys): config 4 — cache grown from 4096 tokens by doubling with device
+  copies while being filled to 131072 tokens, pre-grown to 262144, then 256 sequential
+  single-token steps (batch_rope_int8 append + attention_decode_int8) over L = 131073..131328.
+* roofline: prefill attention kernel against the dense FP16 MFMA peak (2.5 PFLOP/s),
+  decode kernel against HBM (8 TB/s); kernel durations from HIP events on the library's
+  stream over the timed region.
+* cpu_baseline: the C oracle (FP64, the reference's checker arithmetic) on the host cores,
+  on the last 512-query chunk of config 3, extrapolated by the causal flop ratio.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "llm-bootstrap-qwen3.6-35b-dotnet-metal_amd"))
+
+from bootstrap_hip import Device, KernelArgs, engine  # noqa: E402
+
+METRIC = "30K-prefill INT8-KV attn ms/layer (MFMA %); 128K decode KV-read GB/s"
+MFMA_PEAK_TFLOPS = 2500.0      # MI355X dense FP16/BF16
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+OUTLIER_CHANNELS = [30, 31, 62, 63]
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def synthetic(rng, shape, outliers=False):
+    x = rng.standard_normal(shape, dtype=np.float32)
+    if outliers:
+        x[..., OUTLIER_CHANNELS] *= 20
+    return x
+
+
+def upload(device, array):
+    b = device.allocate(array.nbytes)
+    b.write(array)
+    return b
+
+
+def kernel_stats(device, names):
+    stats = {k["kernel"]: k for k in device.read_wall_timing()["kernels"]}
+    out = {}
+    for name in names:
+        if name in stats:
+            out[name] = (stats[name]["gpu_ms"], int(stats[name]["count"]))
+    return out
+
+
+def prefill_flops(pos: int, rows: int) -> float:
+    # 4 * d * H * sum over rows of visible keys (QK and PV, 2 flop per MAC)
+    return 4.0 * 256 * 16 * (rows * pos + rows * (rows + 1) / 2)
+
+
+# --------------------------------------------------------------------------- prefill
+
+class PrefillWorkload:
+    def __init__(self, device, tokens=30720, chunk=512, seed=0):
+        self.device, self.tokens, self.chunk = device, tokens, chunk
+        rng = np.random.default_rng(seed)
+        log(f"prefill: generating {tokens} tokens of synthetic Q/K/V/gate")
+        self.q = upload(device, synthetic(rng, (tokens, 16, 256)))
+        self.k = upload(device, synthetic(rng, (tokens, 2, 256), outliers=True))
+        self.v = upload(device, synthetic(rng, (tokens, 2, 256)))
+        self.gate = upload(device, synthetic(rng, (tokens, 16, 256)))
+        self.rotated = device.allocate(tokens * 4096 * 4)
+        self.cache = engine.Int8KvCache(device, context_window=engine.NATIVE_WINDOW, layers=1)
+        self.cache.ensure_capacity(tokens)
+        self.layer = self.cache.layers[0]
+        self.workspace = engine.DeviceAttentionWorkspace(device)
+        self.workspace.prepare(chunk)
+
+    def step(self):
+        d, layer = self.device, self.layer
+        d.begin()
+        for pos in range(0, self.tokens, self.chunk):
+            rows = min(self.chunk, self.tokens - pos)
+            q = self.q.at(pos * 16384)
+            rot = self.rotated.at(pos * 16384)
+            engine.append_rows(d, layer, q, self.k.at(pos * 2048), self.v.at(pos * 2048), rot, rows, pos)
+            self.workspace.encode_int8(rot, layer.key, layer.value, layer.key_scale, layer.value_scale,
+                                       self.gate.at(pos * 16384), rot, rows, pos)
+        d.end()
+
+    def flops(self):
+        return sum(prefill_flops(pos, min(self.chunk, self.tokens - pos)) for pos in range(0, self.tokens, self.chunk))
+
+
+def cpu_baseline_prefill(work: PrefillWorkload, threads: int):
+    """FP64 oracle over the GPU-built INT8 cache: the last chunk of config 3, extrapolated."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from oracle_lib import Oracle
+    oracle = Oracle()
+    oracle.threads = threads
+    tokens, chunk = work.tokens, work.chunk
+    pos = tokens - chunk
+    layer = work.layer
+    kc = layer.key.read(np.int8, tokens * 512)
+    vc = layer.value.read(np.int8, engine.int8_value_capacity(tokens) * 512)
+    ks = layer.key_scale.read(np.float32, tokens * 2)
+    vs = layer.value_scale.read(np.float32, tokens * 2)
+    q = work.q.read(np.float32, chunk * 4096, pos * 16384).reshape(chunk, 16, 256).astype(np.float64)
+    # partial RoPE of the queries (Int8KvTests.cs:13-18), vectorised; input preparation is not timed
+    angle = (pos + np.arange(chunk))[:, None] * 10_000_000.0 ** (-2.0 * np.arange(32) / 64)
+    c, s = np.cos(angle)[:, None, :], np.sin(angle)[:, None, :]
+    a, b = q[:, :, :32].copy(), q[:, :, 32:64].copy()
+    q[:, :, :32], q[:, :, 32:64] = a * c - b * s, b * c + a * s
+    rot = q.astype(np.float32).ravel()
+    gate = work.gate.read(np.float32, chunk * 4096, pos * 16384)
+    times = []
+    for _ in range(1):
+        t0 = time.perf_counter()
+        oracle.attention(rot, kc, vc, ks, vs, gate, chunk, pos, round_q_half=1)
+        times.append(time.perf_counter() - t0)
+    sample_s = float(np.median(times))
+    ratio = work.flops() / prefill_flops(pos, chunk)
+    return {"value": sample_s * ratio * 1000.0, "unit": "ms/layer", "cores": threads, "kind": "port",
+            "sample": f"FP64 oracle (Int8KvTests.cs:130-157 arithmetic) on the last {chunk}-query chunk "
+                      f"(queries {pos}-{tokens - 1} over {tokens} keys, {sample_s:.2f} s), extrapolated x{ratio:.1f} "
+                      f"by the causal flop ratio to the whole 30720-token layer"}
+
+
+# --------------------------------------------------------------------------- decode
+
+class DecodeWorkload:
+    def __init__(self, device, context=131072, steps=256, seed=1, fill_chunk=8192):
+        self.device, self.context, self.steps = device, context, steps
+        rng = np.random.default_rng(seed)
+        self.cache = engine.Int8KvCache(device, context_window=engine.NATIVE_WINDOW, layers=1)
+        log(f"decode: filling {context} tokens (capacity grows by doubling from {self.cache.capacity})")
+        self.append_ms = 0.0
+        k_all = synthetic(rng, (context + steps, 2, 256), outliers=True)
+        v_all = synthetic(rng, (context + steps, 2, 256))
+        kb, vb = upload(device, k_all[:fill_chunk]), upload(device, v_all[:fill_chunk])
+        for pos in range(0, context, fill_chunk):
+            self.cache.ensure_capacity(pos + fill_chunk)       # PrefillBlock -> EnsureCacheCapacity
+            kb.write(k_all[pos:pos + fill_chunk])
+            vb.write(v_all[pos:pos + fill_chunk])
+            device.begin()
+            engine.store_rows(device, self.cache.layers[0], kb, vb, fill_chunk, pos)
+            device.end()
+        self.cache.ensure_capacity(context + 1)                # pre-grow to 262144 before timing
+        self.growth = list(self.cache.growth_log)
+        kb.dispose()
+        vb.dispose()
+        # one bulk append of the whole history into a second layer: the append roofline sample
+        self.bulk_k = upload(device, k_all[:context])
+        self.bulk_v = upload(device, v_all[:context])
+        self.bulk_layer = engine.Int8KvLayer(device, context)
+        self.q = upload(device, synthetic(rng, (steps, 16, 256)))
+        self.k_new = upload(device, k_all[context:context + steps])
+        self.v_new = upload(device, v_all[context:context + steps])
+        self.gate = upload(device, synthetic(rng, (steps, 16, 256)))
+        self.rotated = device.allocate(steps * 16384)
+        self.out = device.allocate(steps * 16384)
+
+    def run(self):
+        d, layer = self.device, self.cache.layers[0]
+        d.begin()
+        for i in range(self.steps):
+            pos = self.context + i
+            engine.append_rows(d, layer, self.q.at(i * 16384), self.k_new.at(i * 2048), self.v_new.at(i * 2048),
+                               self.rotated.at(i * 16384), 1, pos)
+            engine.decode(d, layer, self.rotated.at(i * 16384), self.gate.at(i * 16384), self.out.at(i * 16384),
+                          pos)
+        d.end()
+
+    def bulk_append(self):
+        d = self.device
+        d.begin()
+        engine.store_rows(d, self.bulk_layer, self.bulk_k, self.bulk_v, self.context, 0)
+        d.end()
+
+    def kv_bytes(self):
+        # 1040 B per attended token: 512 K + 512 V codes + 8 + 8 scale bytes (both KV heads)
+        return sum(1040 * (self.context + i + 1) for i in range(self.steps))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is design-only (DESIGN.md)",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    device = Device()
+    work = PrefillWorkload(device)
+    for _ in range(args.warmup):
+        work.step()
+    device.reset_wall_timing(all_kernels=True)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        work.step()
+    wall_ms = (time.perf_counter() - t0) * 1000.0 / args.steps
+    ks = kernel_stats(device, ["attention_online_int8_q32_k256_r2", "attention_online_int8.combine",
+                               "batch_rope_int8", "attention_query_grouped_half"])
+    attn_ms = ks["attention_online_int8_q32_k256_r2"][0] / args.steps
+    combine_ms = ks.get("attention_online_int8.combine", (0.0, 0))[0] / args.steps
+    launches = ks["attention_online_int8_q32_k256_r2"][1] // args.steps
+    flops = work.flops()
+    achieved = flops / (attn_ms * 1e-3) / 1e12
+    result = {
+        "metric": METRIC, "value": round(wall_ms, 4), "unit": "ms/layer", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(wall_ms, 4), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
+        "config": {"workload": "config 3: 30720-token causal prefill of one full-attention layer, 60 chunks of 512, "
+                               "INT8 KV (append + online attention), 16 Q / 2 KV heads, d=256",
+                   "kv": "int8 + fp32 per-token/head scales", "tokens": 30720, "chunk": 512,
+                   "parallelism": "single GPU"},
+        "prefill": {"attention_kernel_ms_per_layer": round(attn_ms, 4), "combine_ms_per_layer": round(combine_ms, 4),
+                    "append_ms_per_layer": round(ks["batch_rope_int8"][0] / args.steps, 4),
+                    "query_pack_ms_per_layer": round(ks["attention_query_grouped_half"][0] / args.steps, 4),
+                    "attention_launches_per_layer": launches,
+                    "mfma_fraction_end_to_end": round(flops / (wall_ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4)},
+        "roofline": {"bound": "mfma", "kernel": "prefill_int8_kernel (attention_online_int8_q32_k256_r2)",
+                     "achieved": round(achieved, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                     "flops_per_layer": flops},
+    }
+    if not args.no_decode:
+        dec = DecodeWorkload(device)
+        dec.run()  # warm
+        device.reset_wall_timing(all_kernels=True)
+        t0 = time.perf_counter()
+        dec.run()
+        dec_wall = (time.perf_counter() - t0) * 1000.0 / dec.steps
+        kd = kernel_stats(device, ["attention_decode_int8", "attention_decode_int8.combine", "batch_rope_int8"])
+        dec_kernel_ms = kd["attention_decode_int8"][0] / dec.steps
+        dec_comb_ms = kd.get("attention_decode_int8.combine", (0.0, 0))[0] / dec.steps
+        append_ms = kd["batch_rope_int8"][0] / dec.steps
+        bytes_per_step = dec.kv_bytes() / dec.steps
+        dec.bulk_append()
+        device.reset_wall_timing(all_kernels=True)
+        dec.bulk_append()
+        bulk = kernel_stats(device, ["kv_store_int8"])["kv_store_int8"][0]
+        bulk_bytes = 5136.0 * dec.context
+        result["decode"] = {
+            "context": dec.context, "steps": dec.steps, "growth": dec.growth,
+            "kv_read_gbs_step": round(bytes_per_step / (dec_wall * 1e-3) / 1e9, 1),
+            "kv_read_gbs_attention_kernels": round(bytes_per_step / ((dec_kernel_ms + dec_comb_ms) * 1e-3) / 1e9, 1),
+            "ms_per_step_wall": round(dec_wall, 5), "decode_kernel_us": round(dec_kernel_ms * 1000, 3),
+            "combine_kernel_us": round(dec_comb_ms * 1000, 3), "append_kernel_us": round(append_ms * 1000, 3),
+            "bytes_per_step": bytes_per_step,
+        }
+        result["roofline_decode"] = {
+            "bound": "hbm", "kernel": "decode_int8_kernel (attention_decode_int8)",
+            "achieved": round(bytes_per_step / (dec_kernel_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(bytes_per_step / (dec_kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None}
+        result["roofline_append"] = {
+            "bound": "hbm", "kernel": "kv_store_int8 bulk append of 131072 tokens",
+            "achieved": round(bulk_bytes / (bulk * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(bulk_bytes / (bulk * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+            "bytes": bulk_bytes, "kernel_ms": round(bulk, 4)}
+    if not args.no_cpu_baseline:
+        log("cpu baseline: FP64 oracle on the last chunk")
+        result["cpu_baseline"] = cpu_baseline_prefill(work, args.cpu_threads)
+    print(json.dumps(result), flush=True)
+    device.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,243 @@
+"""Host-side KV policy and call sites of the INT8 full-attention path.
+
+The reference engine keeps these in C# (QwenEngine.cs, DeviceAttention.cs,
+ContextLimits.cs, PrefixCache.cs); this module restates exactly those lines over the
+HIP shim so the device path can be driven the way the engine drives it:
+
+* ``ContextLimits``            ContextLimits.cs:5-19
+* ``Int8KvCache``              QwenEngine.cs:17-24,43,61 (allocation), 76-99 (grow by
+                               doubling with a device copy), 122-132 (reset), and
+                               PrefixCache.cs:45-77 (restore = truncate by position, no clear);
+                               ``state_hash`` follows PrefixCacheSelfTest.cs:133-148 (KV part)
+* ``DeviceAttentionWorkspace`` DeviceAttention.cs:14-20 (Prepare), 65-70 (EncodeInt8)
+* ``append_rows`` / ``decode`` the INT8 lines of PrefillBlock (Prefill.cs:248-261) and
+                               Forward (QwenEngine.cs:158-166)
+"""
+from __future__ import annotations
+
+import hashlib
+from typing import List, Optional
+
+import numpy as np
+
+from .native import Binding, Device, GpuBuffer, HipError, KernelArgs
+
+# ContextLimits.cs:5-6
+NATIVE_WINDOW = 262144
+ATTENTION_WORKSPACE_FLOATS = 32 * 1024 * 1024
+# QwenEngine.cs:58-61: layer l is full attention when (l + 1) % 4 == 0 -> 10 of 40
+FULL_ATTENTION_LAYERS = tuple(l for l in range(40) if (l + 1) % 4 == 0)
+KV_HEADS, HEAD_DIM, Q_HEADS, GROUP = 2, 256, 16, 8
+ROPE_THETA = 10_000_000.0
+
+
+class ContextLimits:
+    """ContextLimits.cs:3-20."""
+
+    NativeWindow = NATIVE_WINDOW
+    AttentionWorkspaceFloats = ATTENTION_WORKSPACE_FLOATS
+
+    @staticmethod
+    def output_budget(prompt_tokens: int, requested: int, context_window: int) -> int:
+        if prompt_tokens < 1 or prompt_tokens >= context_window or requested < 1:
+            raise ValueError("Context window exceeded or invalid output budget")
+        return min(requested, context_window - prompt_tokens)
+
+    @staticmethod
+    def prefill_count(position: int, remaining: int) -> int:
+        count = min(512, remaining)
+        return min(count, ATTENTION_WORKSPACE_FLOATS // 16 // (position + count))
+
+
+def validate_context_window(context_window: int) -> int:
+    """QwenEngine.cs:25."""
+    if 1 <= context_window <= NATIVE_WINDOW:
+        return context_window
+    raise ValueError("Context window must fit the model's native 262144-token window")
+
+
+def int8_value_capacity(capacity: int) -> int:
+    """QwenEngine.cs:23: V is allocated in whole 256-token pages."""
+    return (capacity + 255) // 256 * 256
+
+
+def value_index(vector: int, dimension: int) -> int:
+    """kernels.metal:126-128."""
+    token, head = vector // 2, vector % 2
+    return (token // 256 * 2 + head) * 65536 + dimension * 256 + token % 256
+
+
+def grow_schedule(capacity: int, required: int, context: int) -> int:
+    """QwenEngine.cs:85-88: double (capped at the window) until ``required`` fits."""
+    if required <= capacity:
+        return capacity
+    if required > context:
+        raise ValueError("required KV capacity exceeds the context window")
+    while capacity < required:
+        capacity = min(context, capacity * 2)
+    return capacity
+
+
+class Int8KvLayer:
+    """One full-attention layer's INT8 cache: K codes, V pages, K/V scales."""
+
+    def __init__(self, device: Device, capacity: int):
+        self.key = device.allocate(capacity * 512)
+        self.value = device.allocate(int8_value_capacity(capacity) * 512)
+        self.key_scale = device.allocate(capacity * 2 * 4)
+        self.value_scale = device.allocate(capacity * 2 * 4)
+
+    def buffers(self) -> List[GpuBuffer]:
+        return [self.key, self.value, self.key_scale, self.value_scale]
+
+
+class Int8KvCache:
+    """KV allocation / growth / reset / truncate policy of the INT8 target cache."""
+
+    def __init__(self, device: Device, context_window: int = NATIVE_WINDOW, layers: int = 10):
+        self.device = device
+        self.context = validate_context_window(context_window)
+        self.capacity = min(self.context, 4096)                  # QwenEngine.cs:43
+        self.layers = [Int8KvLayer(device, self.capacity) for _ in range(layers)]
+        self.scores = device.allocate(16 * self.capacity * 4)    # QwenEngine.cs:57 (Buffer(16*cap))
+        self.position = 0                                        # consumed tokens of the live lineage
+        self.growth_log: List[int] = []
+
+    @property
+    def target_kv_bytes(self) -> int:
+        """QwenEngine.cs:24 for INT8, scaled to this cache's layer count."""
+        n = len(self.layers)
+        cap = self.capacity
+        return cap * 512 * 2 * n + cap * 2 * 2 * n * 4 + (int8_value_capacity(cap) - cap) * 512 * n
+
+    def _grow(self, buffer: GpuBuffer, nbytes: int) -> GpuBuffer:
+        """QwenEngine.cs:76-82: allocate zero-filled, copy all old bytes, release."""
+        if nbytes <= buffer.length:
+            return buffer
+        replacement = self.device.allocate(nbytes)
+        self.device.copy(replacement, 0, buffer, 0, buffer.length)
+        buffer.dispose()
+        return replacement
+
+    def ensure_capacity(self, required: int) -> None:
+        """QwenEngine.cs:83-99. Must run with no command active (QwenEngine.cs:89)."""
+        capacity = grow_schedule(self.capacity, required, self.context)
+        if capacity == self.capacity:
+            return
+        for layer in self.layers:
+            layer.key = self._grow(layer.key, capacity * 512)
+            layer.value = self._grow(layer.value, int8_value_capacity(capacity) * 512)
+            layer.key_scale = self._grow(layer.key_scale, capacity * 2 * 4)
+            layer.value_scale = self._grow(layer.value_scale, capacity * 2 * 4)
+        self.scores = self._grow(self.scores, capacity * 16 * 4)
+        self.capacity = capacity
+        self.growth_log.append(capacity)
+
+    def reset(self) -> None:
+        """QwenEngine.cs:122-132 (KV part): clear K, V and both scale buffers."""
+        self.device.begin()
+        for layer in self.layers:
+            for buffer in layer.buffers():
+                self.device.clear(buffer)
+        self.device.end()
+        self.position = 0
+
+    def restore_prefix(self, position: int) -> int:
+        """PrefixCache.cs:45-77, KV part: positions at/after the checkpoint are not cleared;
+        causal masking and overwrite-before-read keep them unobservable (PrefixCache.cs:68-70)."""
+        if position < 0 or position > self.position:
+            raise ValueError("checkpoint beyond the live lineage")
+        self.position = position
+        return position
+
+    def state_hash(self, consumed: Optional[int] = None) -> str:
+        """KV part of PrefixTestStateHash (PrefixCacheSelfTest.cs:133-148): K bytes
+        consumed*512, whole V pages plus the consumed prefix of the partial page per
+        (head, d), and the K/V scales consumed*8 bytes; layer by layer."""
+        consumed = self.position if consumed is None else consumed
+        h = hashlib.sha256()
+        pages, tail = consumed // 256, consumed % 256
+        for layer in self.layers:
+            h.update(layer.key.read(np.uint8, consumed * 512).tobytes())
+            h.update(layer.value.read(np.uint8, pages * 256 * 512).tobytes())
+            if tail:
+                block = layer.value.read(np.uint8, 2 * 65536, pages * 2 * 65536).reshape(2, 256, 256)
+                for head in range(2):
+                    for d in range(256):
+                        h.update(block[head, d, :tail].tobytes())
+            h.update(layer.key_scale.read(np.uint8, consumed * 8).tobytes())
+            h.update(layer.value_scale.read(np.uint8, consumed * 8).tobytes())
+        return h.hexdigest()
+
+
+class DeviceAttentionWorkspace:
+    """DeviceAttention.cs:5-72, INT8 part: grouped FP16 query scratch + EncodeInt8."""
+
+    OnlineGroupHeads = 8
+
+    def __init__(self, device: Device):
+        self.device = device
+        self.query: Optional[GpuBuffer] = None
+
+    def prepare(self, rows: int) -> None:
+        """DeviceAttention.cs:14-20 (INT8 needs only the packed query)."""
+        need = rows * 4096 * 2
+        if self.query is None or self.query.length < need:
+            if self.query is not None:
+                self.query.dispose()
+            self.query = self.device.allocate(need)
+
+    @property
+    def packed_query(self) -> GpuBuffer:
+        if self.query is None:
+            raise HipError("Attention is not prepared")
+        return self.query
+
+    def encode_int8(self, q, k, v, ks, vs, gate, output, rows: int, position: int,
+                    prepared_query: bool = False) -> None:
+        """DeviceAttention.cs:65-70. Must be called inside a command."""
+        p = KernelArgs(M=rows, K=position + rows, Position=position, A=self.OnlineGroupHeads)
+        if not prepared_query:
+            self.device.dispatch("attention_query_grouped_half", p, rows * 1024, 128, q, self.packed_query)
+        self.device.dispatch2d("attention_online_int8_q32_k256_r2", p, (rows * 8 + 31) // 32 * 256, 2, 256,
+                               self.packed_query, k, v, gate, output, ks, vs)
+
+    def dispose(self) -> None:
+        if self.query is not None:
+            self.query.dispose()
+            self.query = None
+
+
+def append_rows(device: Device, layer: Int8KvLayer, q, k, v, rotated, rows: int, position: int,
+                theta: float = ROPE_THETA) -> None:
+    """Unfused INT8 append of Prefill.cs:257 / QwenEngine.cs:162: rotate Q into ``rotated``,
+    rotate K and store K/V codes and scales at ``position``. Inside a command."""
+    p = KernelArgs(M=rows, Position=position, K=position + rows, Theta=theta)
+    device.dispatch("batch_rope_int8", p, rows * 4096, 256, q, k, v, rotated,
+                    layer.key, layer.value, layer.key_scale, layer.value_scale)
+
+
+def store_rows(device: Device, layer: Int8KvLayer, k, v, rows: int, position: int) -> None:
+    """Append already-rotated FP32 K/V rows (store_kv_int8 alone). Inside a command."""
+    device.dispatch("kv_store_int8", KernelArgs(M=rows, Position=position), rows * 512, 256,
+                    k, v, layer.key, layer.value, layer.key_scale, layer.value_scale)
+
+
+def decode(device: Device, layer: Int8KvLayer, rotated, gate, output, position: int, rows: int = 1) -> None:
+    """Fused split-K decode over keys [0, position + row] for each row. Inside a command."""
+    p = KernelArgs(M=rows, K=position + rows, Position=position)
+    device.dispatch("attention_decode_int8", p, rows * 4096, 256, rotated, layer.key, layer.value,
+                    gate, output, layer.key_scale, layer.value_scale)
+
+
+def decode_reference_path(device: Device, layer: Int8KvLayer, rotated, gate, output, scores: GpuBuffer,
+                          position: int, rows: int = 1) -> None:
+    """The engine's three-kernel INT8 reader (QwenEngine.cs:163-165, Prefill.cs:280-283)."""
+    length = position + rows
+    p = KernelArgs(M=rows, K=length, Position=position)
+    device.dispatch2d("batch_attention_scores_int8", p, length * 32, rows * 16, 128, rotated, layer.key, scores,
+                      layer.key_scale)
+    soft = KernelArgs(M=rows, K=length, Position=length - 1)
+    device.dispatch("attention_softmax", soft, rows * 16 * 256, 256, scores)
+    device.dispatch("batch_attention_values_int8", p, rows * 4096, 128, scores, layer.value, gate, output,
+                    layer.value_scale)

@@ -1,0 +1,421 @@
+// Single-token (and 1-8 row verification) INT8 attention over the KV cache.
+//
+// Two entry points:
+//   * the reference's three-kernel reader (kernels.metal:147-156,163-166):
+//     batch_attention_scores_int8 -> attention_softmax -> batch_attention_values_int8,
+//     FP32 scores in a caller buffer; serves serial decode and speculative
+//     verification unchanged (QwenEngine.cs:161-165, Prefill.cs:280-285).
+//   * attention_decode_int8: one fused split-K pass that streams the INT8 K/V
+//     pages from HBM once. Scores and PV run on MFMA with FP32-faithful
+//     operands: the FP32 query is split into FP16 hi + lo halves that fill the
+//     16 MFMA columns (8 heads x {hi, lo}), and the scaled probabilities
+//     p*vs[t] likewise into BF16 hi + lo. INT8 codes are dequantized exactly
+//     in registers; scales are applied to scores and probabilities as the
+//     reference does (score = dot * ks[t] / 16, P = p * vs[t]).
+#include "common.h"
+#include "mfma.h"
+
+namespace boot {
+
+
+namespace {
+
+// ---------------------------------------------------------------- reference-compatible reader
+
+// scores[(row*16+h)*K + t] = (q . code) * ks[t*2+h/8] * (1/16), -inf beyond row's
+// causal end (kernels.metal:147-152). One thread per token, eight heads of one
+// KV group per block.
+__global__ __launch_bounds__(64) void scores_int8_kernel(const float *__restrict__ q, const int8_t *__restrict__ k,
+                                                         float *__restrict__ scores, const float *__restrict__ ks,
+                                                         uint32_t rows, uint32_t K, uint32_t pos) {
+    __shared__ float qs[8][256];
+    const uint32_t row = blockIdx.y >> 1, g = blockIdx.y & 1;
+    for (int i = threadIdx.x; i < 8 * 256; i += 64) qs[i / 256][i % 256] = q[(size_t)row * 4096 + (g * 8) * 256 + i];
+    __syncthreads();
+    const uint32_t t = blockIdx.x * 64 + threadIdx.x;
+    if (t >= K) return;
+    float acc[8];
+    const bool visible = t <= pos + row;
+    if (visible) {
+#pragma unroll
+        for (int h = 0; h < 8; h++) acc[h] = 0.0f;
+        const int8_t *kr = k + ((size_t)t * 2 + g) * 256;
+        for (int d0 = 0; d0 < 256; d0 += 16) {
+            const uint4 w = *reinterpret_cast<const uint4 *>(kr + d0);
+            const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const float code = (float)(int8_t)((words[j >> 2] >> (8 * (j & 3))) & 0xff);
+#pragma unroll
+                for (int h = 0; h < 8; h++) acc[h] = fmaf(qs[h][d0 + j], code, acc[h]);
+            }
+        }
+    }
+    const float scale = visible ? ks[(size_t)t * 2 + g] : 0.0f;
+#pragma unroll
+    for (int h = 0; h < 8; h++)
+        scores[((size_t)row * 16 + g * 8 + h) * K + t] = visible ? acc[h] * scale * (1.0f / 16.0f) : -INFINITY;
+}
+
+__device__ inline float block_reduce_256(float v, float *partial, bool is_max) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        float other = __shfl_xor(v, o, 64);
+        v = is_max ? fmaxf(v, other) : v + other;
+    }
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) partial[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float r = partial[0];
+    for (int i = 1; i < 4; i++) r = is_max ? fmaxf(r, partial[i]) : r + partial[i];
+    return r;
+}
+
+// In-place three-pass softmax over i <= pos of each row (kernels.metal:163-166).
+__global__ __launch_bounds__(256) void softmax_kernel(float *__restrict__ x, uint32_t K, uint32_t pos) {
+    __shared__ float partial[4];
+    float *r = x + (size_t)blockIdx.x * K;
+    float top = -INFINITY;
+    for (uint32_t i = threadIdx.x; i <= pos; i += 256) top = fmaxf(top, r[i]);
+    top = block_reduce_256(top, partial, true);
+    float sum = 0.0f;
+    for (uint32_t i = threadIdx.x; i <= pos; i += 256) {
+        const float value = expf(r[i] - top);
+        r[i] = value;
+        sum += value;
+    }
+    sum = block_reduce_256(sum, partial, false);
+    for (uint32_t i = threadIdx.x; i <= pos; i += 256) r[i] /= sum;
+}
+
+// y[(row*16+h)*256+d] = sum_t scores*vs*vcode * sigmoid(gate) (kernels.metal:153-156).
+__global__ __launch_bounds__(256) void values_int8_kernel(const float *__restrict__ scores, const int8_t *__restrict__ v,
+                                                          const float *__restrict__ gate, float *__restrict__ y,
+                                                          const float *__restrict__ vs, uint32_t rows, uint32_t K,
+                                                          uint32_t pos) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * 4096) return;
+    const uint32_t row = i / 4096, h = (i % 4096) / 256, d = i % 256, g = h / 8;
+    const float *s = scores + ((size_t)row * 16 + h) * K;
+    const uint32_t end = pos + row + 1;
+    float sum = 0.0f;
+    uint32_t t = 0;
+    for (; t + 16 <= end && ((t & 255) + 16 <= 256); t += 16) {
+        const uint4 w = *reinterpret_cast<const uint4 *>(v + value_index((uint64_t)t * 2 + g, d));
+        const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const float code = (float)(int8_t)((words[j >> 2] >> (8 * (j & 3))) & 0xff);
+            sum += s[t + j] * vs[(size_t)(t + j) * 2 + g] * code;
+        }
+    }
+    for (; t < end; t++) sum += s[t] * vs[(size_t)t * 2 + g] * (float)v[value_index((uint64_t)t * 2 + g, d)];
+    y[i] = sum * (1.0f / (1.0f + expf(-gate[i])));
+}
+
+// ---------------------------------------------------------------- fused split-K decode
+
+constexpr int kDecodeBlock = 32;       // tokens per wave iteration
+constexpr int kDecodeWaves = 4;
+constexpr int kPartialFloats = 8 * 256 + 16;   // O[8][256], m[8], l[8] per (row, group, split)
+
+struct DecodeParams {
+    const float *q;
+    const int8_t *k;
+    const int8_t *v;
+    const float *ks;
+    const float *vs;
+    const float *gate;
+    float *y;
+    float *partial;
+    uint32_t rows, pos, splits, split_tokens;
+};
+
+__device__ inline float sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// Grid: (splits, 2 KV groups, rows). Each wave walks 32-token blocks of the
+// split; per block it computes S^T[t][n] = K[t] . Qx[n] (16x16x32 FP16 MFMA,
+// n = 8 heads x {hi, lo}), the online softmax for its 8 heads, and
+// O^T[d][n] += V^T[d][t] . Px[t][n] (16x16x32 BF16 MFMA). Lane l holds MFMA
+// column n = l % 16 and token/k group qq = l / 16.
+__global__ __launch_bounds__(256, 2) void decode_int8_kernel(DecodeParams p) {
+    __shared__ float merge_o[kDecodeWaves][8][256];
+    __shared__ float merge_m[kDecodeWaves][8], merge_l[kDecodeWaves][8];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n = lane & 15, qq = lane >> 4, head = n & 7;
+    const bool lo_col = n >= 8;
+    const uint32_t split = blockIdx.x, g = blockIdx.y, row = blockIdx.z;
+    const uint32_t length = p.pos + row + 1;
+    const uint32_t begin = split * p.split_tokens;
+    const uint32_t end = min(length, begin + p.split_tokens);
+
+    // Q^T operands: MFMA c covers dims d(c, qq, e) = 64*(c/2) + 16*qq + 8*(c%2) + e,
+    // matching the 16-byte K loads below.
+    half8 qop[8];
+    {
+        const float *qh = p.q + ((size_t)row * 16 + g * 8 + head) * 256;
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const float *src = qh + 64 * (c >> 1) + 16 * qq + 8 * (c & 1);
+            const float4 a = *reinterpret_cast<const float4 *>(src);
+            const float4 b = *reinterpret_cast<const float4 *>(src + 4);
+            const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const _Float16 hi = (_Float16)x[e];
+                qop[c][e] = lo_col ? (_Float16)(x[e] - (float)hi) : hi;
+            }
+        }
+    }
+
+    floatx4 o[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) o[i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m = -INFINITY, l = 0.0f;
+
+    for (uint32_t t0 = begin + wave * kDecodeBlock; t0 < end; t0 += kDecodeWaves * kDecodeBlock) {
+        // ---- scores: two 16-token tiles; tile a row i holds token t0 + 8*(i/4) + 4*a + i%4,
+        // so after the MFMA lane group qq owns tokens t0 + 8*qq + [0, 8).
+        floatx4 s[2];
+#pragma unroll
+        for (int a = 0; a < 2; a++) {
+            const uint32_t i = lane & 15;
+            uint32_t t = t0 + 8 * (i >> 2) + 4 * a + (i & 3);
+            t = min(t, length - 1);                          // loads stay inside the cache
+            const int8_t *kr = p.k + ((size_t)t * 2 + g) * 256 + 16 * qq;
+            floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint4 w = *reinterpret_cast<const uint4 *>(kr + 64 * j);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_half8(w.x, w.y), qop[2 * j], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_half8(w.z, w.w), qop[2 * j + 1], acc, 0, 0, 0);
+            }
+            s[a] = acc;
+        }
+        // C layout: lane (n, qq) holds rows 4*qq + r -> token t0 + 8*qq + 4*a + r.
+        float sc[8];
+        float top = -INFINITY;
+#pragma unroll
+        for (int a = 0; a < 2; a++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float full = s[a][r] + __shfl_xor(s[a][r], 8, 64);   // hi + lo columns
+                const uint32_t t = t0 + 8 * qq + 4 * a + r;
+                float value = -INFINITY;
+                if (t < end) value = full * p.ks[(size_t)t * 2 + g] * (1.0f / 16.0f);
+                sc[a * 4 + r] = value;
+                top = fmaxf(top, value);
+            }
+        top = fmaxf(top, __shfl_xor(top, 16, 64));
+        top = fmaxf(top, __shfl_xor(top, 32, 64));
+        const float next = fmaxf(m, top);
+        const float decay = expf(m - next);
+        float total = 0.0f;
+        uint32_t pw[4];
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            uint32_t bits[2];
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const uint32_t t = t0 + 8 * qq + e + u;
+                const float prob = expf(sc[e + u] - next);          // 0 for masked tokens
+                total += prob;
+                const float scaled = t < end ? prob * p.vs[(size_t)t * 2 + g] : 0.0f;
+                const uint32_t hi = bf16_bits(scaled);
+                bits[u] = lo_col ? bf16_bits(scaled - bf16_value(hi)) : hi;
+            }
+            pw[e / 2] = bits[0] | (bits[1] << 16);
+        }
+        total += __shfl_xor(total, 16, 64);
+        total += __shfl_xor(total, 32, 64);
+        l = l * decay + total;
+        m = next;
+        if (decay != 1.0f) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) o[i] *= decay;
+        }
+        const bf16x8 pop = __builtin_bit_cast(bf16x8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
+        // ---- values: d-tile dt, lane row d = 16*dt + n, tokens t0 + 8*qq + [0, 8)
+        const uint32_t tv = min(t0 + 8 * qq, length - 1) & ~7u;   // 8-token aligned, inside the cache
+        const int8_t *vbase = p.v + value_index((uint64_t)tv * 2 + g, 0);
+#pragma unroll
+        for (int dt = 0; dt < 16; dt++) {
+            const uint2 w = *reinterpret_cast<const uint2 *>(vbase + (size_t)(16 * dt + n) * 256);
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(i8x8_to_bf16x8(w.x, w.y), pop, o[dt], 0, 0, 0);
+        }
+    }
+
+    // ---- merge the four waves: O^T[d][n] with d = 16*dt + 4*qq + r; heads sum hi + lo columns.
+    if (n < 8) {
+#pragma unroll
+        for (int dt = 0; dt < 16; dt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) merge_o[wave][head][16 * dt + 4 * qq + r] = o[dt][r];
+        if (qq == 0) {
+            merge_m[wave][head] = m;
+            merge_l[wave][head] = l;
+        }
+    }
+    __syncthreads();
+    if (n >= 8) {
+#pragma unroll
+        for (int dt = 0; dt < 16; dt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) merge_o[wave][head][16 * dt + 4 * qq + r] += o[dt][r];
+    }
+    __syncthreads();
+    // thread -> (head h, 8 dims); combine waves with their maxima
+    const int h = threadIdx.x >> 5, d0 = (threadIdx.x & 31) * 8;
+    float mw = -INFINITY;
+    for (int w = 0; w < kDecodeWaves; w++) mw = fmaxf(mw, merge_m[w][h]);
+    float lw = 0.0f, f[kDecodeWaves];
+    for (int w = 0; w < kDecodeWaves; w++) {
+        f[w] = merge_m[w][h] == -INFINITY ? 0.0f : expf(merge_m[w][h] - mw);
+        lw += merge_l[w][h] * f[w];
+    }
+    float acc[8];
+    for (int e = 0; e < 8; e++) {
+        float sum = 0.0f;
+        for (int w = 0; w < kDecodeWaves; w++) sum += merge_o[w][h][d0 + e] * f[w];
+        acc[e] = sum;
+    }
+    if (p.splits == 1) {
+        const size_t at = ((size_t)row * 16 + g * 8 + h) * 256 + d0;
+        for (int e = 0; e < 8; e++) p.y[at + e] = acc[e] / lw * sigmoidf(p.gate[at + e]);
+        return;
+    }
+    float *part = p.partial + (((size_t)row * 2 + g) * p.splits + split) * kPartialFloats;
+    for (int e = 0; e < 8; e++) part[h * 256 + d0 + e] = acc[e];
+    if ((threadIdx.x & 31) == 0) {
+        part[2048 + h] = mw;
+        part[2056 + h] = lw;
+    }
+}
+
+// Merges the splits of one (row, head) slice of 64 dims.
+__global__ __launch_bounds__(64) void decode_combine_kernel(const float *__restrict__ partial, const float *__restrict__ gate,
+                                                            float *__restrict__ y, uint32_t splits) {
+    const uint32_t row = blockIdx.z, hq = blockIdx.y, g = hq / 8, h = hq % 8;
+    const uint32_t d = blockIdx.x * 64 + threadIdx.x;
+    const float *base = partial + ((size_t)row * 2 + g) * splits * kPartialFloats;
+    float mmax = -INFINITY;
+    for (uint32_t s = 0; s < splits; s++) mmax = fmaxf(mmax, base[(size_t)s * kPartialFloats + 2048 + h]);
+    float lsum = 0.0f, osum = 0.0f;
+    for (uint32_t s = 0; s < splits; s++) {
+        const float *part = base + (size_t)s * kPartialFloats;
+        const float ms = part[2048 + h];
+        if (ms == -INFINITY) continue;
+        const float f = expf(ms - mmax);
+        lsum += part[2056 + h] * f;
+        osum += part[h * 256 + d] * f;
+    }
+    const size_t at = ((size_t)row * 16 + hq) * 256 + d;
+    y[at] = osum / lsum * sigmoidf(gate[at]);
+}
+
+inline bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+}  // namespace
+
+const char *launch_scores_int8(Context &c, const View *b, int count, const boot_kernel_args &p, const uint32_t *) {
+    // bindings: q FP32 [rows][16][256], k INT8 cache, scores [rows][16][K], ks (QwenEngine.cs:163, Prefill.cs:280)
+    BOOT_REQUIRE(count >= 4, "batch_attention_scores_int8 needs 4 bindings: q, k, scores, ks");
+    const uint64_t rows = p.m, K = p.k;
+    if (rows == 0 || K == 0) return nullptr;
+    const uint64_t length = std::min<uint64_t>(K, (uint64_t)p.pos + rows);  // keys actually read
+    BOOT_REQUIRE(b[0].bytes >= rows * 16384, "query buffer smaller than rows*4096 floats");
+    BOOT_REQUIRE(b[1].bytes >= length * 512, "K cache smaller than the attended length");
+    BOOT_REQUIRE(b[2].bytes >= rows * 16 * K * 4, "scores buffer smaller than rows*16*K floats");
+    BOOT_REQUIRE(b[3].bytes >= length * 8, "K scale buffer smaller than the attended length");
+    BOOT_REQUIRE(aligned(b[0].ptr, 4) && aligned(b[1].ptr, 16) && aligned(b[2].ptr, 4) && aligned(b[3].ptr, 4),
+                 "bindings misaligned");
+    dim3 grid((uint32_t)((K + 63) / 64), (uint32_t)(rows * 2));
+    scores_int8_kernel<<<grid, 64, 0, context_stream(c)>>>((const float *)b[0].ptr, (const int8_t *)b[1].ptr,
+                                                           (float *)b[2].ptr, (const float *)b[3].ptr, (uint32_t)rows,
+                                                           (uint32_t)K, p.pos);
+    return nullptr;
+}
+
+const char *launch_softmax(Context &c, const View *b, int count, const boot_kernel_args &p, const uint32_t *grid) {
+    // bindings: x scores [groups][K]; groups = dispatched threads / 256 (QwenEngine.cs:164, Prefill.cs:282)
+    BOOT_REQUIRE(count >= 1, "attention_softmax needs 1 binding: scores");
+    BOOT_REQUIRE(grid[3] == 256 && grid[1] <= 1 && grid[2] <= 1, "attention_softmax is dispatched as groups of 256 threads");
+    const uint64_t groups = grid[0] / 256, K = p.k;
+    if (groups == 0) return nullptr;
+    BOOT_REQUIRE(p.pos < K, "softmax position must be below the row stride K");
+    BOOT_REQUIRE(b[0].bytes >= groups * K * 4, "scores buffer smaller than groups*K floats");
+    BOOT_REQUIRE(aligned(b[0].ptr, 4), "scores binding misaligned");
+    softmax_kernel<<<(uint32_t)groups, 256, 0, context_stream(c)>>>((float *)b[0].ptr, (uint32_t)K, p.pos);
+    return nullptr;
+}
+
+const char *launch_values_int8(Context &c, const View *b, int count, const boot_kernel_args &p, const uint32_t *) {
+    // bindings: scores, v INT8 pages, gate, y, vs (QwenEngine.cs:165, Prefill.cs:283)
+    BOOT_REQUIRE(count >= 5, "batch_attention_values_int8 needs 5 bindings: scores, v, gate, y, vs");
+    const uint64_t rows = p.m, K = p.k;
+    if (rows == 0) return nullptr;
+    const uint64_t length = (uint64_t)p.pos + rows;
+    BOOT_REQUIRE(length <= K, "causal end pos+rows exceeds the score row stride K");
+    BOOT_REQUIRE(b[0].bytes >= rows * 16 * K * 4, "scores buffer smaller than rows*16*K floats");
+    BOOT_REQUIRE(b[1].bytes >= value_bytes(length), "V cache smaller than whole pages of the attended length");
+    BOOT_REQUIRE(b[2].bytes >= rows * 16384 && b[3].bytes >= rows * 16384, "gate/output smaller than rows*4096 floats");
+    BOOT_REQUIRE(b[4].bytes >= length * 8, "V scale buffer smaller than the attended length");
+    BOOT_REQUIRE(aligned(b[1].ptr, 16), "V cache binding must be 16-byte aligned");
+    const uint64_t threads = rows * 4096;
+    values_int8_kernel<<<(uint32_t)((threads + 255) / 256), 256, 0, context_stream(c)>>>(
+        (const float *)b[0].ptr, (const int8_t *)b[1].ptr, (const float *)b[2].ptr, (float *)b[3].ptr,
+        (const float *)b[4].ptr, (uint32_t)rows, (uint32_t)K, p.pos);
+    return nullptr;
+}
+
+const char *launch_decode_int8(Context &c, const View *b, int count, const boot_kernel_args &p, const uint32_t *) {
+    // bindings (EncodeInt8 order, DeviceAttention.cs:69): q FP32 [rows][16][256] (rotated),
+    // k, v, gate, y, ks, vs. Row r attends t <= pos + r.
+    BOOT_REQUIRE(count >= 7, "attention_decode_int8 needs 7 bindings: q, k, v, gate, y, ks, vs");
+    const uint64_t rows = p.m;
+    if (rows == 0) return nullptr;
+    BOOT_REQUIRE(rows <= 64, "attention_decode_int8 serves at most 64 rows");
+    const uint64_t length = (uint64_t)p.pos + rows;
+    BOOT_REQUIRE(length <= 262144, "attended length exceeds the 262144-token window");
+    BOOT_REQUIRE(b[0].bytes >= rows * 16384, "query buffer smaller than rows*4096 floats");
+    BOOT_REQUIRE(b[1].bytes >= length * 512, "K cache smaller than the attended length");
+    BOOT_REQUIRE(b[2].bytes >= value_bytes(length), "V cache smaller than whole pages of the attended length");
+    BOOT_REQUIRE(b[3].bytes >= rows * 16384 && b[4].bytes >= rows * 16384, "gate/output smaller than rows*4096 floats");
+    BOOT_REQUIRE(b[5].bytes >= length * 8 && b[6].bytes >= length * 8, "KV scale buffers smaller than the attended length");
+    BOOT_REQUIRE(aligned(b[0].ptr, 16) && aligned(b[1].ptr, 16) && aligned(b[2].ptr, 16) && aligned(b[3].ptr, 4) &&
+                     aligned(b[4].ptr, 4) && aligned(b[5].ptr, 4) && aligned(b[6].ptr, 4),
+                 "bindings misaligned (q, k, v need 16 bytes)");
+    // Split the longest row's keys so that about two blocks run per CU.
+    const uint32_t per_split_min = kDecodeWaves * kDecodeBlock;   // 128 tokens
+    const uint64_t target_blocks = (uint64_t)std::max(1, context_cus(c)) * 2;
+    uint64_t splits = std::max<uint64_t>(1, target_blocks / (2 * rows));
+    uint64_t split_tokens = (length + splits - 1) / splits;
+    split_tokens = std::max<uint64_t>(per_split_min, (split_tokens + per_split_min - 1) / per_split_min * per_split_min);
+    splits = (length + split_tokens - 1) / split_tokens;
+    DecodeParams d;
+    d.q = (const float *)b[0].ptr;
+    d.k = (const int8_t *)b[1].ptr;
+    d.v = (const int8_t *)b[2].ptr;
+    d.gate = (const float *)b[3].ptr;
+    d.y = (float *)b[4].ptr;
+    d.ks = (const float *)b[5].ptr;
+    d.vs = (const float *)b[6].ptr;
+    d.rows = (uint32_t)rows;
+    d.pos = p.pos;
+    d.splits = (uint32_t)splits;
+    d.split_tokens = (uint32_t)split_tokens;
+    d.partial = nullptr;
+    if (splits > 1) {
+        d.partial = (float *)context_workspace(c, rows * 2 * splits * kPartialFloats * sizeof(float));
+        BOOT_REQUIRE(d.partial, "cannot allocate decode split workspace");
+    }
+    decode_int8_kernel<<<dim3((uint32_t)splits, 2, (uint32_t)rows), 256, 0, context_stream(c)>>>(d);
+    if (splits > 1) {
+        context_split(c, "attention_decode_int8.combine");
+        decode_combine_kernel<<<dim3(4, 16, (uint32_t)rows), 64, 0, context_stream(c)>>>(d.partial, d.gate, d.y,
+                                                                                        (uint32_t)splits);
+    }
+    return nullptr;
+}
+
+}  // namespace boot

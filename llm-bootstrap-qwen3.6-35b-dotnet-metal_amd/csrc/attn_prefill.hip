@@ -1,0 +1,369 @@
+// Causal online GQA prefill over the INT8 KV cache (block prefill, <= 512-token
+// chunks), MFMA on gfx950.
+//
+// Reference semantics: attention_int8_prefill / attention_online_int8_q32_k256_r2
+// (kernels.metal:1378-1457), dispatched by DeviceAttentionWorkspace.EncodeInt8
+// (DeviceAttention.cs:65-70):
+//   s[r][t] = (q16[r] . kcode[t]) * (1/16) * ks[t]        FP16 Q x INT8 K, FP32 accumulate
+//   online max / sum over t <= pos + r/8 (FP32 statistics, l sums unscaled e)
+//   P[r][t] = bf16(e * vs[t]);  o = o * decay + P . vcode  BF16 x INT8 V, FP32 accumulate
+//   y = o / l * sigmoid(gate)
+// One deliberate change: the scaled probabilities are rounded to FP16 after
+// dividing the V scales by their maximum over the work-group's key range
+// (vs_ref), and vs_ref multiplies the result once at the end. e * vs / vs_ref
+// lies in [0, 1], so FP16 cannot underflow where it matters (the reason the
+// reference chose BF16, docs/INT8_KV_20261104.md:16) and its rounding is 8x
+// finer than BF16's, which keeps the output within rel-L2 1e-3 of FP64 where
+// BF16 probabilities measure 1.6e-3 to 3.2e-3.
+// Logical row r of KV group g is (token r/8, head 8g + r%8): the grouped FP16
+// query layout of attention_query_grouped_half (kernels.metal:1276-1281).
+//
+// gfx950 structure (not the Metal tiling): a work-group of 4 waves owns 128
+// logical rows (16 tokens x 8 heads) of one KV group, each wave 32 rows. Per
+// 64-key step the work-group dequantizes the INT8 K tile and the V page slice
+// to FP16 once into LDS (codes are exact), then every wave computes
+// S^T = K . Q^T and O^T += V^T . P^T with v_mfma_f32_32x32x16_f16.
+// Transposed products put one query row per lane column, so row statistics are
+// per-lane and the accumulator rescale needs no cross-lane traffic; the key
+// order inside each QK tile is permuted so a lane's S registers are exactly
+// its FP16 B operand for the PV product. The exponentials run in the base-2
+// domain (the K scale carries log2(e)/16). Long histories split the key range
+// across work-groups (split-K) and a combine kernel merges (m, l, O).
+#include "common.h"
+#include "mfma.h"
+
+namespace boot {
+
+
+namespace {
+
+constexpr int kRows = 128;                 // logical rows per work-group
+constexpr int kKeys = 64;                  // keys per step
+constexpr int kKStride = 256 + 8;          // FP16 K tile row stride (halves): 528 bytes
+constexpr int kVStride = kKeys + 8;        // FP16 V^T tile row stride (halves): 144 bytes
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct PrefillParams {
+    const _Float16 *q;      // grouped FP16 [2][M][8][256]
+    const int8_t *k;        // [cap][2][256]
+    const int8_t *v;        // V pages
+    const float *gate;      // [M][16][256]
+    float *y;               // [M][16][256]
+    const float *ks, *vs;   // [cap][2]
+    float *partial;         // split workspace
+    uint32_t rows;          // M tokens in the chunk
+    uint32_t pos;           // history
+    uint32_t keys;          // K = pos + M
+    uint32_t tiles;         // 128-row tiles per group
+    uint32_t splits;
+    uint32_t split_keys;    // multiple of kKeys
+    uint32_t remap;         // 1: XCD-aware block order
+};
+
+constexpr size_t kPartialStride = (size_t)kRows * 256 + 2 * kRows;   // O^T rows + m + l
+
+__device__ inline float sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// Key row of QK tile row i: bits 2 and 3 of i swapped (see header comment).
+__device__ inline int qk_key_row(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
+
+__global__ __launch_bounds__(256, 2) void prefill_int8_kernel(PrefillParams p) {
+    __shared__ __attribute__((aligned(16))) _Float16 klds[kKeys * kKStride];
+    __shared__ __attribute__((aligned(16))) _Float16 vlds[256 * kVStride];
+    __shared__ float kscale[kKeys], vscale[kKeys];
+    __shared__ float vs_partial[4];
+
+    // ---- block -> (group, tile, split); XCD-aware: blocks sharing a key range
+    // (same group and split) land on the same XCD (round-robin dispatch).
+    uint32_t b = blockIdx.x, g, tile, split;
+    {
+        const uint32_t combos = 2 * p.splits;
+        uint32_t combo;
+        if (p.remap) {
+            const uint32_t xcd = b % 8, idx = b / 8;
+            combo = xcd + 8 * (idx / p.tiles);
+            tile = idx % p.tiles;
+        } else {
+            combo = b / p.tiles;
+            tile = b % p.tiles;
+        }
+        (void)combos;
+        g = combo % 2;
+        split = combo / 2;
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int i = lane & 31, kk = lane >> 5;
+    const uint32_t R = p.rows * 8;
+    const uint32_t r0 = tile * kRows;
+    const uint32_t my_row = r0 + 32 * wave + i;
+    const bool row_valid = my_row < R;
+    const uint32_t rr = row_valid ? my_row : R - 1;
+    const uint32_t limit = p.pos + rr / 8;                              // keys <= limit visible
+    const uint32_t tile_last = min(R - 1, r0 + kRows - 1);
+    const uint32_t tile_end = p.pos + tile_last / 8 + 1;               // keys [0, tile_end)
+    const uint32_t kbeg = split * p.split_keys;
+    const uint32_t kend = min(tile_end, kbeg + p.split_keys);
+    const uint32_t wave_first = min(R - 1, r0 + 32 * wave);
+    const uint32_t wave_min_limit = p.pos + wave_first / 8;
+
+    // ---- Q^T operands (B of the QK product): lane (i, kk), dims 16c + 8kk + [0, 8)
+    half8 qop[16];
+    {
+        const _Float16 *qrow = p.q + ((size_t)g * R + rr) * 256 + 8 * kk;
+#pragma unroll
+        for (int c = 0; c < 16; c++) qop[c] = *reinterpret_cast<const half8 *>(qrow + 16 * c);
+    }
+
+    // ---- vs_ref: the largest V scale over this block's keys (0 if all are 0)
+    const int tid = threadIdx.x;
+    float vs_ref = 0.0f;
+    for (uint32_t key = kbeg + tid; key < kend; key += 256) vs_ref = fmaxf(vs_ref, p.vs[(size_t)key * 2 + g]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) vs_ref = fmaxf(vs_ref, __shfl_xor(vs_ref, o, 64));
+    if (lane == 0) vs_partial[wave] = vs_ref;
+    __syncthreads();
+    vs_ref = fmaxf(fmaxf(vs_partial[0], vs_partial[1]), fmaxf(vs_partial[2], vs_partial[3]));
+    const float vs_inv = vs_ref > 0.0f ? 1.0f / vs_ref : 0.0f;
+
+    floatx16 o[8];
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) o[dt][v] = 0.0f;
+    float m = -INFINITY, l = 0.0f;
+
+    for (uint32_t key0 = kbeg; key0 < kend; key0 += kKeys) {
+        __syncthreads();   // previous tile fully consumed
+        // ---- stage K: 64 keys x 256 codes -> FP16; thread: key key0 + tid/4, 64 codes
+        {
+            const int krow = tid >> 2, part = tid & 3;
+            const uint32_t key = min(key0 + krow, p.keys - 1);
+            const uint4 *src = reinterpret_cast<const uint4 *>(p.k + ((size_t)key * 2 + g) * 256 + part * 64);
+            uint4 *dst = reinterpret_cast<uint4 *>(klds + krow * kKStride + part * 64);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint4 w = src[j];
+                uint32_t h[8];
+                i8x4_to_f16(w.x, h[0], h[1]);
+                i8x4_to_f16(w.y, h[2], h[3]);
+                i8x4_to_f16(w.z, h[4], h[5]);
+                i8x4_to_f16(w.w, h[6], h[7]);
+                dst[2 * j] = make_uint4(h[0], h[1], h[2], h[3]);
+                dst[2 * j + 1] = make_uint4(h[4], h[5], h[6], h[7]);
+            }
+        }
+        // ---- stage V^T: 256 dims x 64 keys of the page slice -> FP16
+        {
+            const int8_t *page = p.v + value_index((uint64_t)key0 * 2 + g, 0);
+#pragma unroll
+            for (int it = 0; it < 4; it++) {
+                const int d = it * 64 + (tid >> 2), part = tid & 3;
+                const uint4 w = *reinterpret_cast<const uint4 *>(page + (size_t)d * 256 + part * 16);
+                uint32_t h[8];
+                i8x4_to_f16(w.x, h[0], h[1]);
+                i8x4_to_f16(w.y, h[2], h[3]);
+                i8x4_to_f16(w.z, h[4], h[5]);
+                i8x4_to_f16(w.w, h[6], h[7]);
+                uint4 *dst = reinterpret_cast<uint4 *>(vlds + d * kVStride + part * 16);
+                dst[0] = make_uint4(h[0], h[1], h[2], h[3]);
+                dst[1] = make_uint4(h[4], h[5], h[6], h[7]);
+            }
+        }
+        if (tid < kKeys) {
+            const uint32_t key = key0 + tid;
+            const bool inside = key < p.keys;   // poisoned tails beyond K never reach P
+            kscale[tid] = inside ? p.ks[(size_t)key * 2 + g] * (kLog2e / 16.0f) : 0.0f;
+            vscale[tid] = inside ? p.vs[(size_t)key * 2 + g] * vs_inv : 0.0f;
+        }
+        __syncthreads();
+
+        // ---- S^T = K . Q^T, two 32-key tiles
+        floatx16 s[2];
+#pragma unroll
+        for (int a = 0; a < 2; a++) {
+            floatx16 acc;
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[v] = 0.0f;
+            const _Float16 *krow = klds + (32 * a + qk_key_row(i)) * kKStride + 8 * kk;
+#pragma unroll
+            for (int c = 0; c < 16; c++)
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8 *>(krow + 16 * c), qop[c],
+                                                             acc, 0, 0, 0);
+            s[a] = acc;
+        }
+
+        // ---- online softmax for this lane's row; lane value v of tile a is key
+        // key0 + 32a + 16(v/8) + 8kk + v%8.
+        const bool masking = key0 + kKeys - 1 > wave_min_limit;
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int a = 0; a < 2; a++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int local = 32 * a + 16 * (v >> 3) + 8 * kk + (v & 7);
+                float x = s[a][v] * kscale[local];
+                if (masking && key0 + local > limit) x = -INFINITY;
+                s[a][v] = x;
+                tmax = fmaxf(tmax, x);
+            }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float mnew = fmaxf(m, tmax);
+        const float mref = mnew == -INFINITY ? 0.0f : mnew;
+        const float decay = __builtin_amdgcn_exp2f(m - mref);
+        float rowsum = 0.0f;
+        uint32_t pw[2][8];
+#pragma unroll
+        for (int a = 0; a < 2; a++)
+#pragma unroll
+            for (int v = 0; v < 16; v += 2) {
+                const int local = 32 * a + 16 * (v >> 3) + 8 * kk + (v & 7);
+                const float e0 = __builtin_amdgcn_exp2f(s[a][v] - mref);
+                const float e1 = __builtin_amdgcn_exp2f(s[a][v + 1] - mref);
+                rowsum += e0 + e1;
+                const half2v ph = {(_Float16)(e0 * vscale[local]), (_Float16)(e1 * vscale[local + 1])};   // RNE
+                pw[a][v / 2] = __builtin_bit_cast(uint32_t, ph);
+            }
+        rowsum += __shfl_xor(rowsum, 32, 64);
+        l = l * decay + rowsum;
+        m = mnew;
+        if (__ballot(decay != 1.0f)) {
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) o[dt] *= decay;
+        }
+
+        // ---- O^T += V^T . P^T; PV step u takes keys 16u + 8kk + [0, 8) = tile u/2, values 8(u%2)..
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const half8 pb = __builtin_bit_cast(
+                half8, make_uint4(pw[u >> 1][4 * (u & 1)], pw[u >> 1][4 * (u & 1) + 1], pw[u >> 1][4 * (u & 1) + 2],
+                                  pw[u >> 1][4 * (u & 1) + 3]));
+            const _Float16 *vrow = vlds + i * kVStride + 16 * u + 8 * kk;
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++)
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                    *reinterpret_cast<const half8 *>(vrow + 32 * dt * kVStride), pb, o[dt], 0, 0, 0);
+        }
+    }
+
+    // ---- epilogue: lane (i, kk) holds O^T[d][row] for d = 32dt + 8(v/4) + 4kk + v%4
+    if (p.splits == 1) {
+        if (!row_valid) return;
+        const uint32_t token = my_row / 8, head = g * 8 + my_row % 8;
+        const size_t base = ((size_t)token * 16 + head) * 256;
+        const float inv = vs_ref / l;
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+            for (int vq = 0; vq < 4; vq++) {
+                const int d = 32 * dt + 8 * vq + 4 * kk;
+                const float4 gv = *reinterpret_cast<const float4 *>(p.gate + base + d);
+                float4 out;
+                out.x = o[dt][4 * vq + 0] * inv * sigmoidf(gv.x);
+                out.y = o[dt][4 * vq + 1] * inv * sigmoidf(gv.y);
+                out.z = o[dt][4 * vq + 2] * inv * sigmoidf(gv.z);
+                out.w = o[dt][4 * vq + 3] * inv * sigmoidf(gv.w);
+                *reinterpret_cast<float4 *>(p.y + base + d) = out;
+            }
+        return;
+    }
+    float *part = p.partial + (((size_t)g * p.tiles + tile) * p.splits + split) * kPartialStride;
+    const int local_row = 32 * wave + i;
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++) o[dt] *= vs_ref;
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+        for (int vq = 0; vq < 4; vq++) {
+            const int d = 32 * dt + 8 * vq + 4 * kk;
+            *reinterpret_cast<float4 *>(part + (size_t)local_row * 256 + d) =
+                make_float4(o[dt][4 * vq], o[dt][4 * vq + 1], o[dt][4 * vq + 2], o[dt][4 * vq + 3]);
+        }
+    if (kk == 0) {
+        part[(size_t)kRows * 256 + local_row] = m;
+        part[(size_t)kRows * 256 + kRows + local_row] = l;
+    }
+}
+
+// One block per (group, tile, logical row); thread d merges the splits.
+__global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillParams p) {
+    const uint32_t local_row = blockIdx.x, tile = blockIdx.y, g = blockIdx.z;
+    const uint32_t row = tile * kRows + local_row;
+    if (row >= p.rows * 8) return;
+    const float *base = p.partial + ((size_t)g * p.tiles + tile) * p.splits * kPartialStride;
+    float mmax = -INFINITY;
+    for (uint32_t s = 0; s < p.splits; s++) mmax = fmaxf(mmax, base[s * kPartialStride + (size_t)kRows * 256 + local_row]);
+    const int d = threadIdx.x;
+    float lsum = 0.0f, osum = 0.0f;
+    for (uint32_t s = 0; s < p.splits; s++) {
+        const float *part = base + s * kPartialStride;
+        const float ms = part[(size_t)kRows * 256 + local_row];
+        if (ms == -INFINITY) continue;
+        const float f = __builtin_amdgcn_exp2f(ms - mmax);
+        lsum += part[(size_t)kRows * 256 + kRows + local_row] * f;
+        osum += part[(size_t)local_row * 256 + d] * f;
+    }
+    const uint32_t token = row / 8, head = g * 8 + row % 8;
+    const size_t at = ((size_t)token * 16 + head) * 256 + d;
+    p.y[at] = osum / lsum * sigmoidf(p.gate[at]);
+}
+
+inline bool aligned(const void *ptr, uintptr_t a) { return (reinterpret_cast<uintptr_t>(ptr) & (a - 1)) == 0; }
+
+}  // namespace
+
+const char *launch_online_int8(Context &c, const View *b, int count, const boot_kernel_args &a, const uint32_t *) {
+    // bindings (DeviceAttention.cs:69): q FP16 grouped, k, v, gate, y, ks, vs; M rows, K = pos + M,
+    // Position = pos, A = 8 heads per group.
+    BOOT_REQUIRE(count >= 7, "attention_online_int8 needs 7 bindings: q, k, v, gate, y, ks, vs");
+    const uint64_t rows = a.m;
+    if (rows == 0) return nullptr;
+    BOOT_REQUIRE(a.a == 8 || a.a == 0, "INT8 online attention groups 8 query heads per KV head (A = 8)");
+    BOOT_REQUIRE((uint64_t)a.k == (uint64_t)a.pos + rows, "K must equal Position + M");
+    const uint64_t keys = a.k;
+    BOOT_REQUIRE(keys <= 262144, "attended length exceeds the 262144-token window");
+    BOOT_REQUIRE(b[0].bytes >= rows * 8192, "packed FP16 query smaller than rows*4096 halves");
+    BOOT_REQUIRE(b[1].bytes >= keys * 512, "K cache smaller than K tokens");
+    BOOT_REQUIRE(b[2].bytes >= value_bytes(keys), "V cache smaller than whole pages of K tokens");
+    BOOT_REQUIRE(b[3].bytes >= rows * 16384 && b[4].bytes >= rows * 16384, "gate/output smaller than rows*4096 floats");
+    BOOT_REQUIRE(b[5].bytes >= keys * 8 && b[6].bytes >= keys * 8, "KV scale buffers smaller than K tokens");
+    BOOT_REQUIRE(aligned(b[0].ptr, 16) && aligned(b[1].ptr, 16) && aligned(b[2].ptr, 16) && aligned(b[3].ptr, 16) &&
+                     aligned(b[4].ptr, 16) && aligned(b[5].ptr, 4) && aligned(b[6].ptr, 4),
+                 "bindings misaligned (q, k, v, gate, y need 16 bytes)");
+    PrefillParams p;
+    p.q = (const _Float16 *)b[0].ptr;
+    p.k = (const int8_t *)b[1].ptr;
+    p.v = (const int8_t *)b[2].ptr;
+    p.gate = (const float *)b[3].ptr;
+    p.y = (float *)b[4].ptr;
+    p.ks = (const float *)b[5].ptr;
+    p.vs = (const float *)b[6].ptr;
+    p.rows = (uint32_t)rows;
+    p.pos = a.pos;
+    p.keys = (uint32_t)keys;
+    p.tiles = (uint32_t)((rows * 8 + kRows - 1) / kRows);
+    // split-K: enough blocks for two per CU, each split at least 256 keys
+    const uint64_t base_blocks = 2ull * p.tiles;
+    const uint64_t want = 2ull * (uint64_t)std::max(1, context_cus(c));
+    uint64_t splits = std::max<uint64_t>(1, (want + base_blocks - 1) / base_blocks);
+    splits = std::min<uint64_t>(splits, std::max<uint64_t>(1, keys / 256));
+    uint64_t split_keys = (keys + splits - 1) / splits;
+    split_keys = (split_keys + kKeys - 1) / kKeys * kKeys;
+    splits = (keys + split_keys - 1) / split_keys;
+    p.splits = (uint32_t)splits;
+    p.split_keys = (uint32_t)split_keys;
+    const uint64_t blocks = base_blocks * splits;
+    p.remap = ((2 * splits) % 8 == 0) ? 1u : 0u;
+    p.partial = nullptr;
+    if (splits > 1) {
+        p.partial = (float *)context_workspace(c, base_blocks * splits * kPartialStride * sizeof(float));
+        BOOT_REQUIRE(p.partial, "cannot allocate prefill split workspace");
+    }
+    prefill_int8_kernel<<<(uint32_t)blocks, 256, 0, context_stream(c)>>>(p);
+    if (splits > 1) {
+        context_split(c, "attention_online_int8.combine");
+        prefill_combine_kernel<<<dim3(kRows, p.tiles, 2), 256, 0, context_stream(c)>>>(p);
+    }
+    return nullptr;
+}
+
+}  // namespace boot

@@ -1,0 +1,299 @@
+/*
+ * kvref — CPU restatement of the reference INT8 KV-cache semantics.
+ * TEST INFRASTRUCTURE ONLY (the checker, never the product). See kvref.h for the
+ * per-function reference citations and what pins each function.
+ *
+ * Build: oracle/Makefile (gcc -O2 -ffp-contract=off; no fast-math, so every
+ * float expression below is a single IEEE round-to-nearest operation).
+ */
+#include "kvref.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+uint64_t kvref_value_index(uint32_t vector, uint32_t dimension) {
+    /* kernels.metal:126-128: token=vector/2, head=vector%2;
+     * ((token/256)*2+head)*65536 + dimension*256 + token%256 */
+    uint64_t token = vector / 2u, head = vector % 2u;
+    return ((token / 256u) * 2u + head) * 65536u + (uint64_t)dimension * 256u + token % 256u;
+}
+
+uint64_t kvref_value_bytes(uint32_t length) {
+    /* Int8KvTests.cs:11: ((length+255)/256*256)*512 */
+    return ((uint64_t)length + 255u) / 256u * 256u * 512u;
+}
+
+void kvref_quantize(const float *x, int8_t *codes, float *scale) {
+    /* kernels.metal:135-140 / Int8KvTests.cs:116-118 */
+    float amax = 0.0f;
+    for (int d = 0; d < 256; d++) {
+        float a = fabsf(x[d]);
+        if (a > amax) amax = a;
+    }
+    volatile float s = amax / 127.0f;          /* fp32 RN division */
+    *scale = s;
+    if (!(amax > 0.0f)) {
+        for (int d = 0; d < 256; d++) codes[d] = 0;
+        return;
+    }
+    volatile float r = 127.0f / amax;          /* fp32 RN division */
+    for (int d = 0; d < 256; d++) {
+        volatile float p = x[d] * r;           /* one fp32 RN multiply */
+        float c = rintf(p);                    /* default mode: round half to even */
+        if (c > 127.0f) c = 127.0f;
+        if (c < -127.0f) c = -127.0f;
+        codes[d] = (int8_t)c;
+    }
+}
+
+void kvref_store(const float *k, const float *v, int rows, int pos,
+                 int8_t *kc, int8_t *vc, float *ks, float *vs) {
+    int8_t codes[256];
+    float scale;
+    for (int row = 0; row < rows; row++) {
+        for (int h = 0; h < 2; h++) {
+            uint32_t vector = (uint32_t)(pos + row) * 2u + (uint32_t)h;
+            kvref_quantize(k + ((size_t)row * 2 + h) * 256, codes, &scale);
+            ks[vector] = scale;
+            memcpy(kc + (size_t)vector * 256, codes, 256);
+            kvref_quantize(v + ((size_t)row * 2 + h) * 256, codes, &scale);
+            vs[vector] = scale;
+            for (int d = 0; d < 256; d++) vc[kvref_value_index(vector, (uint32_t)d)] = codes[d];
+        }
+    }
+}
+
+double kvref_rotate_f64(const float *x, int d, int position) {
+    /* Int8KvTests.cs:13-18 */
+    if (d >= 64) return x[d];
+    int j = d % 32;
+    double angle = position * pow(10000000.0, -2.0 * j / 64);
+    return d < 32 ? x[j] * cos(angle) - x[j + 32] * sin(angle)
+                  : x[j + 32] * cos(angle) + x[j] * sin(angle);
+}
+
+uint16_t kvref_half_bits(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) return (uint16_t)(sign | 0x7c00u | (ax > 0x7f800000u ? 0x200u : 0u));
+    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);      /* >= 65520 rounds to inf */
+    if (ax < 0x38800000u) {                                        /* below 2^-14: subnormal */
+        float a;
+        memcpy(&a, &ax, 4);
+        return (uint16_t)(sign | (uint32_t)rintf(a * 16777216.0f)); /* exact scale, RNE */
+    }
+    uint32_t h = (((ax >> 23) - 112u) << 10) | ((ax & 0x7fffffu) >> 13);
+    uint32_t rem = ax & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+    return (uint16_t)(sign | h);
+}
+
+float kvref_half_to_float(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 31u, m = h & 1023u, x;
+    if (e == 0) {
+        float r = (float)m * (1.0f / 16777216.0f);
+        return (h & 0x8000u) ? -r : r;
+    }
+    if (e == 31) x = sign | 0x7f800000u | (m << 13);
+    else x = sign | ((e + 112u) << 23) | (m << 13);
+    float r;
+    memcpy(&r, &x, 4);
+    return r;
+}
+
+float kvref_bf16_round(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    if ((x & 0x7fffffffu) > 0x7f800000u) x |= 0x00400000u;   /* quiet NaN */
+    else x += 0x7fffu + ((x >> 16) & 1u);
+    x &= 0xffff0000u;
+    float r;
+    memcpy(&r, &x, 4);
+    return r;
+}
+
+void kvref_query_grouped_half(const float *x, int rows, int group, uint16_t *y) {
+    /* kernels.metal:1276-1281: logical=at/256, block=logical/(M*A), local=logical%(M*A),
+     * row=local/A, head=block*A+local%A; y[at]=half(x[(row*16+head)*256+d]) */
+    for (int64_t logical = 0; logical < (int64_t)rows * 16; logical++) {
+        int64_t block = logical / ((int64_t)rows * group), local = logical % ((int64_t)rows * group);
+        int64_t row = local / group, head = block * group + local % group;
+        for (int d = 0; d < 256; d++) y[logical * 256 + d] = kvref_half_bits(x[(row * 16 + head) * 256 + d]);
+    }
+}
+
+/* ---------------------------------------------------------------- attention */
+
+typedef struct {
+    const float *q;
+    int round_q_half;
+    const int8_t *kc, *vc;
+    const float *ks, *vs, *gate;
+    const uint16_t *kh, *vh;   /* FP16 control cache when non-NULL */
+    int rows, pos;
+    double *out, *bound;
+    int64_t next, total;       /* work items = rows*16 */
+    pthread_mutex_t lock;
+} attn_job;
+
+static void attend_one(attn_job *j, int row, int head, double *logits) {
+    int length = j->pos + row + 1, g = head / 8;
+    double q[256];
+    for (int d = 0; d < 256; d++) {
+        float value = j->q[((size_t)row * 16 + head) * 256 + d];
+        q[d] = j->round_q_half ? (double)kvref_half_to_float(kvref_half_bits(value)) : (double)value;
+    }
+    double maxv = -INFINITY;
+    for (int t = 0; t < length; t++) {
+        double acc = 0;
+        size_t at = ((size_t)t * 2 + g) * 256;
+        if (j->kh) {
+            for (int d = 0; d < 256; d++) acc += q[d] * (double)kvref_half_to_float(j->kh[at + d]) / 16;
+        } else {
+            /* Int8KvTests.cs:137: query * code * ks / 16, accumulated in FP64 */
+            double ks = j->ks[(size_t)t * 2 + g];
+            for (int d = 0; d < 256; d++) acc += q[d] * j->kc[at + d] * ks / 16;
+        }
+        logits[t] = acc;
+        if (acc > maxv) maxv = acc;
+    }
+    double sum = 0;
+    for (int t = 0; t < length; t++) {
+        logits[t] = exp(logits[t] - maxv);
+        sum += logits[t];
+    }
+    double *o = j->out + ((size_t)row * 16 + head) * 256;
+    double *b = j->bound ? j->bound + ((size_t)row * 16 + head) * 256 : NULL;
+    double acc[256], mag[256];
+    for (int d = 0; d < 256; d++) acc[d] = mag[d] = 0;
+    for (int t = 0; t < length; t++) {
+        double p = logits[t] / sum;
+        uint32_t vector = (uint32_t)t * 2u + (uint32_t)g;
+        if (j->vh) {
+            for (int d = 0; d < 256; d++) acc[d] += p * (double)kvref_half_to_float(j->vh[(size_t)vector * 256 + d]);
+        } else {
+            /* Int8KvTests.cs:147: exp/sum * vcode * vs */
+            double vs = j->vs[vector];
+            uint64_t page = kvref_value_index(vector, 0);
+            for (int d = 0; d < 256; d++) {
+                double c = p * j->vc[page + (uint64_t)d * 256u] * vs;
+                acc[d] += c;
+                mag[d] += fabs(c);
+            }
+        }
+    }
+    for (int d = 0; d < 256; d++) {
+        /* Int8KvTests.cs:151-152: expected / (1 + exp(-gate)) */
+        double gv = 1.0 + exp(-(double)j->gate[((size_t)row * 16 + head) * 256 + d]);
+        o[d] = acc[d] / gv;
+        if (b) b[d] = mag[d] / gv;
+    }
+}
+
+static void *attn_worker(void *arg) {
+    attn_job *j = (attn_job *)arg;
+    double *logits = (double *)malloc(sizeof(double) * ((size_t)j->pos + j->rows + 1));
+    for (;;) {
+        pthread_mutex_lock(&j->lock);
+        int64_t item = j->next++;
+        pthread_mutex_unlock(&j->lock);
+        if (item >= j->total) break;
+        attend_one(j, (int)(item / 16), (int)(item % 16), logits);
+    }
+    free(logits);
+    return NULL;
+}
+
+static void run_attention(attn_job *j, int threads) {
+    j->next = 0;
+    j->total = (int64_t)j->rows * 16;
+    pthread_mutex_init(&j->lock, NULL);
+    if (threads < 1) threads = 1;
+    if (threads > 256) threads = 256;
+    pthread_t tid[256];
+    int started = 0;
+    for (int i = 1; i < threads; i++)
+        if (pthread_create(&tid[started], NULL, attn_worker, j) == 0) started++;
+    attn_worker(j);
+    for (int i = 0; i < started; i++) pthread_join(tid[i], NULL);
+    pthread_mutex_destroy(&j->lock);
+}
+
+void kvref_attention_f64(const float *q, int round_q_half,
+                         const int8_t *kc, const int8_t *vc,
+                         const float *ks, const float *vs, const float *gate,
+                         int rows, int pos, double *out, double *bound, int threads) {
+    attn_job j;
+    memset(&j, 0, sizeof j);
+    j.q = q; j.round_q_half = round_q_half; j.kc = kc; j.vc = vc; j.ks = ks; j.vs = vs;
+    j.gate = gate; j.rows = rows; j.pos = pos; j.out = out; j.bound = bound;
+    run_attention(&j, threads);
+}
+
+void kvref_attention_fp16kv_f64(const float *q, int round_q_half,
+                                const uint16_t *kh, const uint16_t *vh, const float *gate,
+                                int rows, int pos, double *out, int threads) {
+    attn_job j;
+    memset(&j, 0, sizeof j);
+    j.q = q; j.round_q_half = round_q_half; j.kh = kh; j.vh = vh;
+    j.gate = gate; j.rows = rows; j.pos = pos; j.out = out;
+    run_attention(&j, threads);
+}
+
+/* ---------------------------------------------------------------- generators */
+
+void kvref_fill_hash(float *out, int64_t count, uint32_t seed, float scale) {
+    /* FastAttentionTests.cs:111-119 */
+    for (int64_t i = 0; i < count; i++) {
+        uint32_t h = (uint32_t)i + seed * 0x9e3779b9u;
+        h ^= h >> 16;
+        h *= 0x7feb352du;
+        h ^= h >> 15;
+        volatile float centered = (float)(h & 65535u) - 32768.0f;
+        volatile float unit = centered / 49157.0f;
+        out[i] = unit * scale;
+    }
+}
+
+static uint64_t splitmix64(uint64_t *state) {
+    uint64_t z = (*state += 0x9e3779b97f4a7c15ull);
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+static double uniform01(uint64_t *state) {
+    return ((double)(splitmix64(state) >> 11) + 0.5) * (1.0 / 9007199254740992.0);
+}
+
+static void normal_pair(uint64_t *state, double *a, double *b) {
+    double u1 = uniform01(state), u2 = uniform01(state);
+    double r = sqrt(-2.0 * log(u1)), th = 6.283185307179586476925286766559 * u2;
+    *a = r * cos(th);
+    *b = r * sin(th);
+}
+
+void kvref_normal(float *out, int64_t count, uint64_t seed) {
+    uint64_t state = seed;
+    for (int64_t i = 0; i < count; i += 2) {
+        double a, b;
+        normal_pair(&state, &a, &b);
+        out[i] = (float)a;
+        if (i + 1 < count) out[i + 1] = (float)b;
+    }
+}
+
+void kvref_student_t4(float *out, int64_t count, uint64_t seed) {
+    uint64_t state = seed;
+    for (int64_t i = 0; i < count; i++) {
+        double n[6];
+        normal_pair(&state, &n[0], &n[1]);
+        normal_pair(&state, &n[2], &n[3]);
+        normal_pair(&state, &n[4], &n[5]);
+        double chi2 = n[1] * n[1] + n[2] * n[2] + n[3] * n[3] + n[4] * n[4];
+        out[i] = (float)(n[0] / sqrt(chi2 / 4.0));
+    }
+}

@@ -1,0 +1,200 @@
+"""INT8 online attention parity on the GPU against the FP64 oracle.
+
+Prefill (attention_online_int8_*): the case list, inputs, guards, alias and bounds of
+Int8KvTests.Attention (Int8KvTests.cs:93-181) plus the north-star bar
+rel-L2 <= 1e-3 and max-abs <= 2e-3 against FP64 over the dequantized cache with FP16 Q.
+Decode (attention_decode_int8 and the reference three-kernel reader): FP32 Q, same bar."""
+import numpy as np
+import pytest
+
+from bootstrap_hip import KernelArgs
+from kvcase import outlier_kv, poison_tail, reference_kv, rel_l2, upload, upload_cache
+
+pytestmark = pytest.mark.gpu
+
+REL_L2, MAX_ABS = 1e-3, 2e-3
+
+
+def build_case(oracle, history, rows, kv=None):
+    length = history + rows
+    k, v = kv if kv is not None else reference_kv(length)
+    kc, vc, ks, vs = oracle.empty_cache(length + 1)
+    oracle.store(k, v, 0, kc, vc, ks, vs)
+    poison_tail(oracle, kc, vc, ks, vs, length)
+    q = oracle.fill_hash(rows * 4096, 17, 3)
+    gate = oracle.fill_hash(rows * 4096, 11, 1)
+    return q, gate, (kc, vc, ks, vs)
+
+
+def run_prefill(device, q, gate, cache, rows, history, alias=False, kernel="attention_online_int8_q32_k256_r2"):
+    qb = upload(device, q, extra_bytes=4)
+    gb = upload(device, gate)
+    packed = device.allocate(rows * 4096 * 2)
+    out = qb if alias else device.allocate(q.nbytes + 4)
+    if not alias:
+        out.write(np.full(rows * 4096 + 1, np.nan, np.float32))
+    p = KernelArgs(M=rows, K=history + rows, Position=history, A=8)
+    device.begin()
+    device.dispatch("attention_query_grouped_half", p, rows * 1024, 128, qb, packed)
+    device.dispatch2d(kernel, p, (rows * 8 + 31) // 32 * 256, 2, 256, packed, cache.kc, cache.vc, gb, out, cache.ks,
+                      cache.vs)
+    device.end()
+    y = out.read(np.float32, rows * 4096 + 1)
+    for b in {id(x): x for x in (qb, gb, packed, out)}.values():
+        b.dispose()
+    return y
+
+
+PREFILL_CASES = [(0, 1), (17, 7), (127, 31), (127, 32), (257, 33), (4093, 7), (8192, 128), (0, 512), (3584, 512),
+                 (30000, 33)]
+
+
+@pytest.mark.parametrize("history,rows", PREFILL_CASES)
+def test_prefill_matches_fp64(device, oracle, history, rows):
+    q, gate, host = build_case(oracle, history, rows)
+    cache = upload_cache(device, *host)
+    y = run_prefill(device, q, gate, cache, rows, history)
+    assert np.isnan(y[-1]), "output guard overwritten"                          # Int8KvTests.cs:127
+    y = y[:-1]
+    assert np.all(np.isfinite(y)), "nonfinite INT8 attention"                  # Int8KvTests.cs:126
+    ref, bound = oracle.attention(q, *host, gate, rows, history, round_q_half=1, with_bound=True)
+    err = np.abs(y - ref)
+    assert rel_l2(y, ref) <= REL_L2 and err.max() <= MAX_ABS, (rel_l2(y, ref), err.max())
+    # BF16 probability rounding bound of the reference (Int8KvTests.cs:154-156)
+    assert np.all(err <= bound / 256 + 1e-4)
+    # in-place: output aliases the FP32 query buffer (Int8KvTests.cs:128-129)
+    y2 = run_prefill(device, q, gate, cache, rows, history, alias=True)[:-1]
+    assert np.array_equal(y2.view(np.uint32), y.view(np.uint32))
+    cache.dispose()
+
+
+def test_prefill_kernel_aliases_agree(device, oracle):
+    """The r2, r1 and K128 names of the reference are serviced by the same gfx950 kernel."""
+    q, gate, host = build_case(oracle, 257, 33)
+    cache = upload_cache(device, *host)
+    outs = [run_prefill(device, q, gate, cache, 33, 257, kernel=name)
+            for name in ("attention_online_int8_q32_k256_r2", "attention_online_int8", "attention_online_int8_q32_k128")]
+    assert all(np.array_equal(outs[0][:-1].view(np.uint32), o[:-1].view(np.uint32)) for o in outs[1:])
+    cache.dispose()
+
+
+def test_prefill_small_value_scale(device, oracle):
+    """V scales x 1e-6 scale the output by 1e-6 within 0.8% (Int8KvTests.cs:171-181)."""
+    q, gate, host = build_case(oracle, 0, 1)
+    cache = upload_cache(device, *host)
+    y = run_prefill(device, q, gate, cache, 1, 0)[:-1]
+    kc, vc, ks, vs = host
+    small = vs.copy()
+    small[:2] *= np.float32(1e-6)
+    cache.vs.write(small)
+    y_small = run_prefill(device, q, gate, cache, 1, 0)[:-1]
+    magnitude = np.abs(y).max()
+    assert np.all(np.abs(y_small / 1e-6 - y) < magnitude * 0.008 + 1e-6)
+    cache.dispose()
+
+
+def test_config2_chunked_prefill(device, oracle):
+    """Config 2: 4096-token causal prompt in 8 chunks of 512 with outlier K channels; the cache
+    is appended on the GPU chunk by chunk and every chunk is checked against FP64."""
+    total, chunk = 4096, 512
+    k, v = outlier_kv(oracle, total, seed=20)
+    q_all = oracle.normal(total * 4096, 22)
+    gate_all = np.zeros(total * 4096, np.float32)
+    kc, vc, ks, vs = oracle.empty_cache(total)
+    cache = upload_cache(device, kc, vc, ks, vs)
+    worst_rel, worst_abs = 0.0, 0.0
+    for c in range(total // chunk):
+        pos = c * chunk
+        kb, vb = upload(device, k[pos:pos + chunk]), upload(device, v[pos:pos + chunk])
+        device.begin()
+        device.dispatch("kv_store_int8", KernelArgs(M=chunk, Position=pos), chunk * 512, 256, kb, vb, cache.kc,
+                        cache.vc, cache.ks, cache.vs)
+        device.end()
+        kb.dispose()
+        vb.dispose()
+        q = q_all[pos * 4096:(pos + chunk) * 4096]
+        gate = gate_all[pos * 4096:(pos + chunk) * 4096]
+        y = run_prefill(device, q, gate, cache, chunk, pos)[:-1]
+        oracle.store(k[pos:pos + chunk], v[pos:pos + chunk], pos, kc, vc, ks, vs)
+        if c in (0, 3, 7):
+            ref = oracle.attention(q, kc, vc, ks, vs, gate, chunk, pos, round_q_half=1)
+            worst_rel = max(worst_rel, rel_l2(y, ref))
+            worst_abs = max(worst_abs, float(np.abs(y - ref).max()))
+            # the GPU-appended cache is byte-identical to the oracle's
+            assert cache.kc.read(np.int8, (pos + chunk) * 512).tobytes() == kc[:(pos + chunk) * 512].tobytes()
+    assert worst_rel <= REL_L2 and worst_abs <= MAX_ABS, (worst_rel, worst_abs)
+    cache.dispose()
+
+
+# ------------------------------------------------------------------------------- decode
+
+def run_decode(device, q, gate, cache, rows, history, path="fused", length_cap=None):
+    qb, gb = upload(device, q), upload(device, gate)
+    out = device.allocate(q.nbytes + 4)
+    out.write(np.full(rows * 4096 + 1, np.nan, np.float32))
+    length = history + rows
+    device.begin()
+    if path == "fused":
+        device.dispatch("attention_decode_int8", KernelArgs(M=rows, K=length, Position=history), rows * 4096, 256,
+                        qb, cache.kc, cache.vc, gb, out, cache.ks, cache.vs)
+    else:
+        scores = device.allocate(rows * 16 * length * 4)
+        p = KernelArgs(M=rows, K=length, Position=history)
+        device.dispatch2d("batch_attention_scores_int8", p, length * 32, rows * 16, 128, qb, cache.kc, scores,
+                          cache.ks)
+        device.dispatch("attention_softmax", KernelArgs(M=rows, K=length, Position=length - 1), rows * 16 * 256, 256,
+                        scores)
+        device.dispatch("batch_attention_values_int8", p, rows * 4096, 128, scores, cache.vc, gb, out, cache.vs)
+    device.end()
+    y = out.read(np.float32, rows * 4096 + 1)
+    for b in (qb, gb, out):
+        b.dispose()
+    if path != "fused":
+        scores.dispose()
+    return y
+
+
+DECODE_CASES = [(0, 1), (1, 1), (17, 7), (127, 1), (255, 1), (256, 1), (4093, 7), (8191, 1), (30000, 1), (65535, 2)]
+
+
+@pytest.mark.parametrize("path", ["fused", "reference"])
+@pytest.mark.parametrize("history,rows", DECODE_CASES)
+def test_decode_matches_fp64(device, oracle, history, rows, path):
+    if path == "reference" and history > 10000:
+        pytest.skip("three-kernel reader checked on shorter histories")
+    q, gate, host = build_case(oracle, history, rows)
+    cache = upload_cache(device, *host)
+    y = run_decode(device, q, gate, cache, rows, history, path=path)
+    assert np.isnan(y[-1])
+    y = y[:-1]
+    assert np.all(np.isfinite(y))
+    ref = oracle.attention(q, *host, gate, rows, history, round_q_half=0)
+    err = np.abs(y - ref)
+    assert rel_l2(y, ref) <= REL_L2 and err.max() <= MAX_ABS, (rel_l2(y, ref), err.max())
+    cache.dispose()
+
+
+def test_decode_fused_vs_reference_reader(device, oracle):
+    """The fused decode and the engine's scalar reader agree (Int8KvTests.cs:159-170 bound)."""
+    history, rows = 4093, 7
+    q, gate, host = build_case(oracle, history, rows)
+    cache = upload_cache(device, *host)
+    a = run_decode(device, q, gate, cache, rows, history, path="fused")[:-1]
+    b = run_decode(device, q, gate, cache, rows, history, path="reference")[:-1]
+    assert np.max(np.abs(a - b)) < 4.1e-3
+    cache.dispose()
+
+
+def test_decode_long_context_outliers(device, oracle):
+    """Decode at 131072 context over N(0,1) + outlier K channels (config 4 distribution)."""
+    length = 131072
+    k, v = outlier_kv(oracle, length, seed=40)
+    kc, vc, ks, vs = oracle.empty_cache(length)
+    oracle.store(k, v, 0, kc, vc, ks, vs)
+    cache = upload_cache(device, kc, vc, ks, vs)
+    q = oracle.normal(4096, 41)
+    gate = oracle.normal(4096, 42)
+    y = run_decode(device, q, gate, cache, 1, length - 1)[:-1]
+    ref = oracle.attention(q, kc, vc, ks, vs, gate, 1, length - 1, round_q_half=0)
+    assert rel_l2(y, ref) <= REL_L2 and np.abs(y - ref).max() <= MAX_ABS
+    cache.dispose()

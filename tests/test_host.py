@@ -1,0 +1,72 @@
+"""CPU-side checks: the C ABI library loads and exports every declared symbol, and the
+host KV policy mirrors the engine's constants and rules (Program.cs:307-320)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    names = []
+    for header in os.listdir(os.path.join(ROOT, "include")):
+        if header.endswith(".h"):
+            text = open(os.path.join(ROOT, "include", header)).read()
+            text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+            names += re.findall(r"\b(boot_[a-z_0-9]+)\s*\(", text)
+    return sorted(set(names))
+
+
+def test_library_exports_every_declared_symbol():
+    from bootstrap_hip import native
+    lib = ctypes.CDLL(native.library_path())
+    declared = declared_functions()
+    assert len(declared) >= 20
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(native.SIGNATURES) == set(declared)
+
+
+def test_kernel_args_layout():
+    from bootstrap_hip import KernelArgs
+    assert ctypes.sizeof(KernelArgs) == 64
+    assert KernelArgs.Epsilon.offset == 32 and KernelArgs.C.offset == 48
+
+
+def test_context_limits_rules():
+    from bootstrap_hip import ContextLimits, validate_context_window
+    for valid in (1, 512, 4096, 8192, 32768, 32769, 262144):                   # Program.cs:307
+        assert validate_context_window(valid) == valid
+    for invalid in (-1, 0, 262145, 2 ** 31 - 1):                               # Program.cs:308-312
+        with pytest.raises(ValueError):
+            validate_context_window(invalid)
+    for position in (0, 4090, 32760, 65530, 262144 - 513):                     # Program.cs:313-318
+        count = ContextLimits.prefill_count(position, 512)
+        assert 1 <= count <= 512 and count * 16 * (position + count) <= ContextLimits.AttentionWorkspaceFloats
+    assert ContextLimits.output_budget(10, 65536, 262144) == 65536             # Program.cs:319
+    assert ContextLimits.output_budget(10, 2 ** 31 - 1, 32768) == 32758
+    assert ContextLimits.output_budget(32767, 99999, 32768) == 1
+
+
+def test_grow_schedule_doubles_to_window():
+    from bootstrap_hip import grow_schedule
+    cap, seen = 4096, []
+    while cap < 262144:
+        cap = grow_schedule(cap, cap + 1, 262144)
+        seen.append(cap)
+    assert seen == [8192, 16384, 32768, 65536, 131072, 262144]
+    assert grow_schedule(4096, 131073, 262144) == 262144
+    assert grow_schedule(4096, 5000, 6000) == 6000                             # capped at the window
+    with pytest.raises(ValueError):
+        grow_schedule(4096, 262145, 262144)
+
+
+def test_target_kv_bytes_full_window():
+    from bootstrap_hip import int8_value_capacity
+    cap, layers = 262144, 10
+    # QwenEngine.cs:24 for INT8: K and V codes + FP32 K/V scales + V page padding
+    total = cap * 512 * 2 * layers + cap * 2 * 2 * layers * 4 + (int8_value_capacity(cap) - cap) * 512 * layers
+    assert total == 2_726_297_600
+    assert int8_value_capacity(4097) == 4352 and int8_value_capacity(4096) == 4096

@@ -1,0 +1,237 @@
+"""Pins the CPU oracle (oracle/kvref.c) against independent implementations, closed forms
+and the reference's own known-answer checks. CPU only."""
+import numpy as np
+import pytest
+
+
+def np_quantize(x):
+    """Independent NumPy float32 restatement of kernels.metal:135-140 / Int8KvTests.cs:116-118."""
+    x = np.asarray(x, np.float32)
+    amax = np.max(np.abs(x))
+    scale = np.float32(amax) / np.float32(127.0)
+    if amax == 0:
+        return np.zeros(256, np.int8), np.float32(scale)
+    recip = np.float32(127.0) / np.float32(amax)
+    codes = np.clip(np.rint(x * recip), -127, 127).astype(np.int8)
+    return codes, np.float32(scale)
+
+
+def test_quantize_matches_numpy_bitwise(oracle):
+    rng = np.random.default_rng(1)
+    for trial in range(2000):
+        kind = trial % 5
+        if kind == 0:
+            x = rng.standard_normal(256).astype(np.float32)
+        elif kind == 1:
+            x = (rng.standard_t(4, 256) * 10).astype(np.float32)
+        elif kind == 2:
+            x = rng.uniform(-3, 3, 256).astype(np.float32)
+            x[rng.integers(0, 256)] = -17.0
+        elif kind == 3:
+            x = (rng.standard_normal(256) * 1e-6).astype(np.float32)
+        else:
+            x = (rng.integers(-254, 255, 256) / 2).astype(np.float32)  # many exact .5 ties
+        codes, scale = oracle.quantize(x)
+        ref_codes, ref_scale = np_quantize(x)
+        assert scale.tobytes() == ref_scale.tobytes()
+        assert np.array_equal(codes, ref_codes)
+
+
+def test_quantize_special_cases(oracle):
+    zero = np.zeros(256, np.float32)
+    codes, scale = oracle.quantize(zero)
+    assert scale == 0 and not codes.any()                     # Int8KvTests.cs:60
+    neg_zero = -zero
+    codes, scale = oracle.quantize(neg_zero)
+    assert scale == 0 and not codes.any()
+    x = np.zeros(256, np.float32)
+    x[:6] = [127.0, 2.5, 3.5, -2.5, -3.5, 0.5]                  # amax 127 -> recip exactly 1
+    codes, scale = oracle.quantize(x)
+    assert scale == np.float32(1.0)
+    assert list(codes[:6]) == [127, 2, 4, -2, -4, 0]           # round half to even
+    rng = np.random.default_rng(7)
+    for _ in range(200):
+        x = rng.standard_normal(256).astype(np.float32) * rng.uniform(1e-3, 1e3)
+        codes, scale = oracle.quantize(x)
+        i = np.argmax(np.abs(x))
+        assert codes[i] == (127 if x[i] > 0 else -127)         # the amax element maps to +-127
+        assert codes.min() >= -127                             # never -128
+        err = np.abs(codes.astype(np.float64) * scale - x)
+        # |c*s - x| <= s/2 up to the rounding of s and 127/amax
+        assert np.all(err <= scale * 0.5 * (1 + 1e-5) + np.spacing(np.abs(x)))
+
+
+def test_value_index_is_page_transposed_bijection(oracle):
+    length = 512
+    seen = np.zeros(oracle.value_bytes(length), np.int32)
+    for vector in range(length * 2):
+        for d in (0, 1, 77, 255):
+            seen[oracle.value_index(vector, d)] += 1
+    # full bijection for all dims via a vectorised sweep of a few vectors
+    offsets = set()
+    for vector in range(0, length * 2):
+        base = oracle.value_index(vector, 0)
+        offsets.update(range(base, base + 256 * 256, 256))
+    assert len(offsets) == length * 2 * 256 == oracle.value_bytes(length)
+    # consecutive tokens at fixed (head, d) are adjacent bytes inside a page
+    assert oracle.value_index(2 * 5 + 1, 9) + 1 == oracle.value_index(2 * 6 + 1, 9)
+    # token t and t+256 are one (page, 2 heads) block apart; heads are 65536 apart
+    assert oracle.value_index(2 * 300, 3) - oracle.value_index(2 * 44, 3) == 2 * 65536
+    assert oracle.value_index(2 * 44 + 1, 3) - oracle.value_index(2 * 44, 3) == 65536
+    assert oracle.value_bytes(1) == 256 * 512 and oracle.value_bytes(257) == 512 * 512   # Int8KvTests.cs:11
+
+
+def test_store_layout(oracle):
+    rng = np.random.default_rng(3)
+    rows, pos = 37, 250
+    k = rng.standard_normal((rows, 2, 256)).astype(np.float32)
+    v = rng.standard_normal((rows, 2, 256)).astype(np.float32)
+    kc, vc, ks, vs = oracle.empty_cache(pos + rows, fill=0x55)
+    oracle.store(k, v, pos, kc, vc, ks, vs)
+    for row in range(rows):
+        for h in range(2):
+            vector = (pos + row) * 2 + h
+            ck, sk = np_quantize(k[row, h])
+            cv, sv = np_quantize(v[row, h])
+            assert np.array_equal(kc[vector * 256:(vector + 1) * 256], ck) and ks[vector] == sk
+            got_v = np.array([vc[oracle.value_index(vector, d)] for d in range(256)], np.int8)
+            assert np.array_equal(got_v, cv) and vs[vector] == sv
+    assert np.all(kc[:pos * 512].view(np.uint8) == 0x55)       # prefix untouched (Int8KvTests.cs:64-68)
+
+
+def test_half_rounding_matches_numpy(oracle):
+    rng = np.random.default_rng(5)
+    values = np.concatenate([
+        rng.standard_normal(4000).astype(np.float32) * 10,
+        (rng.standard_normal(2000) * 1e-5).astype(np.float32),            # subnormal halves
+        np.array([65504, 65519.99, 65520, 70000, -65520, 6.1035156e-05, 5.96e-8, 2.98e-8, 0.0, -0.0,
+                  1 + 2 ** -11, 1 + 3 * 2 ** -11, 2049, 2051], np.float32),
+    ])
+    for value in values:
+        assert oracle.half_bits(float(value)) == int(np.float32(value).astype(np.float16).view(np.uint16))
+
+
+def test_bf16_rounding_matches_torch(oracle):
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(9)
+    values = np.concatenate([rng.standard_normal(3000) * 100, rng.standard_normal(1000) * 1e-30]).astype(np.float32)
+    ref = torch.from_numpy(values).to(torch.bfloat16).to(torch.float32).numpy()
+    got = np.array([oracle.bf16_round(float(v)) for v in values], np.float32)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_rotate_closed_forms(oracle):
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal(256).astype(np.float32)
+    assert np.array_equal(oracle.rotate_vector_f64(x, 0), x.astype(np.float64))     # position 0
+    for position in (1, 4093, 131071, 262143):
+        r = oracle.rotate_vector_f64(x, position)
+        assert np.array_equal(r[64:], x[64:].astype(np.float64))                     # passthrough
+        j = np.arange(32)
+        angle = position * 10_000_000.0 ** (-2.0 * j / 64)
+        z = (x[j].astype(np.float64) + 1j * x[j + 32]) * np.exp(1j * angle)          # complex form
+        assert np.allclose(r[:32], z.real, atol=1e-12) and np.allclose(r[32:64], z.imag, atol=1e-12)
+        assert np.allclose(r[:32] ** 2 + r[32:64] ** 2, x[:32].astype(np.float64) ** 2 + x[32:64] ** 2)
+
+
+def np_attention(q, kc, vc, ks, vs, gate, rows, pos, round_q):
+    """Independent NumPy float64 attention over the dequantized cache."""
+    length = pos + rows
+    qv = q.reshape(rows, 16, 256).astype(np.float64)
+    if round_q:
+        qv = q.reshape(rows, 16, 256).astype(np.float16).astype(np.float64)
+    K = kc[:length * 512].reshape(length, 2, 256).astype(np.float64) * ks[:length * 2].reshape(length, 2, 1)
+    pages = vc.reshape(-1, 2, 256, 256)
+    V = np.zeros((length, 2, 256))
+    for t in range(length):
+        V[t] = pages[t // 256, :, :, t % 256].astype(np.float64) * vs[t * 2:t * 2 + 2].reshape(2, 1)
+    out = np.zeros((rows, 16, 256))
+    for r in range(rows):
+        n = pos + r + 1
+        for h in range(16):
+            s = K[:n, h // 8] @ qv[r, h] / 16
+            p = np.exp(s - s.max())
+            p /= p.sum()
+            out[r, h] = p @ V[:n, h // 8]
+    return (out / (1 + np.exp(-gate.reshape(rows, 16, 256).astype(np.float64)))).ravel()
+
+
+@pytest.mark.parametrize("history,rows", [(0, 1), (17, 7), (255, 3)])
+def test_attention_matches_numpy(oracle, history, rows):
+    rng = np.random.default_rng(history + rows)
+    length = history + rows
+    k = rng.uniform(-3, 3, (length, 2, 256)).astype(np.float32)
+    v = rng.uniform(-1, 1, (length, 2, 256)).astype(np.float32)
+    kc, vc, ks, vs = oracle.empty_cache(length)
+    oracle.store(k, v, 0, kc, vc, ks, vs)
+    q = oracle.fill_hash(rows * 4096, 17, 3)
+    gate = oracle.fill_hash(rows * 4096, 11, 1)
+    for round_q in (0, 1):
+        got = oracle.attention(q, kc, vc, ks, vs, gate, rows, history, round_q)
+        ref = np_attention(q, kc, vc, ks, vs, gate, rows, history, round_q)
+        assert np.allclose(got, ref, rtol=1e-12, atol=1e-13)
+
+
+def test_attention_closed_forms(oracle):
+    rng = np.random.default_rng(21)
+    # one key: output = dequantized v * sigmoid(gate)
+    k = rng.standard_normal((1, 2, 256)).astype(np.float32)
+    v = rng.standard_normal((1, 2, 256)).astype(np.float32)
+    kc, vc, ks, vs = oracle.empty_cache(1)
+    oracle.store(k, v, 0, kc, vc, ks, vs)
+    q = rng.standard_normal(4096).astype(np.float32)
+    gate = rng.standard_normal(4096).astype(np.float32)
+    out = oracle.attention(q, kc, vc, ks, vs, gate, 1, 0, 0).reshape(16, 256)
+    for h in range(16):
+        vhat = np.array([vc[oracle.value_index(h // 8, d)] for d in range(256)]) * float(vs[h // 8])
+        assert np.allclose(out[h], vhat / (1 + np.exp(-gate.reshape(16, 256)[h].astype(np.float64))), rtol=1e-12)
+    # identical keys: uniform weights -> mean of dequantized V
+    n = 40
+    k = np.repeat(rng.standard_normal((1, 2, 256)).astype(np.float32), n, axis=0)
+    v = rng.standard_normal((n, 2, 256)).astype(np.float32)
+    kc, vc, ks, vs = oracle.empty_cache(n)
+    oracle.store(k, v, 0, kc, vc, ks, vs)
+    zero_gate = np.zeros(4096, np.float32)
+    out = oracle.attention(q, kc, vc, ks, vs, zero_gate, 1, n - 1, 0).reshape(16, 256)
+    mean = np.zeros((2, 256))
+    for t in range(n):
+        for g in range(2):
+            mean[g] += np.array([vc[oracle.value_index(t * 2 + g, d)] for d in range(256)]) * float(vs[t * 2 + g])
+    mean /= n
+    assert np.allclose(out[0], mean[0] * 0.5, rtol=1e-10) and np.allclose(out[9], mean[1] * 0.5, rtol=1e-10)
+    # equal queries inside a KV group give equal outputs
+    q2 = np.tile(rng.standard_normal(256).astype(np.float32), 16)
+    out = oracle.attention(q2, kc, vc, ks, vs, zero_gate, 1, n - 1, 0).reshape(16, 256)
+    assert np.array_equal(out[0], out[7]) and np.array_equal(out[8], out[15])
+
+
+def test_fill_hash_known_values(oracle):
+    # FastAttentionTests.cs:111-119 evaluated with Python integers and NumPy float32
+    def reference(i, seed, scale):
+        h = (i + seed * 0x9E3779B9) & 0xFFFFFFFF
+        h ^= h >> 16
+        h = (h * 0x7FEB352D) & 0xFFFFFFFF
+        h ^= h >> 15
+        return (np.float32(h & 65535) - np.float32(32768)) / np.float32(49157) * np.float32(scale)
+    got = oracle.fill_hash(5000, 17, 3.0)
+    ref = np.array([reference(i, 17, 3.0) for i in range(5000)], np.float32)
+    assert np.array_equal(got, ref)
+    assert np.abs(got).max() <= 3 * 32768 / 49157 + 1e-6
+
+
+def test_query_grouped_half_matches_numpy(oracle):
+    rows = 5
+    x = np.random.default_rng(2).standard_normal(rows * 4096).astype(np.float32) * 3
+    got = oracle.query_grouped_half(x, rows, 8)
+    # [rows][16][256] -> [2 groups][rows][8][256]
+    ref = x.reshape(rows, 2, 8, 256).transpose(1, 0, 2, 3).astype(np.float16).view(np.uint16).ravel()
+    assert np.array_equal(got, ref)
+
+
+def test_generators_are_seeded_and_standard(oracle):
+    a = oracle.normal(200000, 0)
+    assert np.array_equal(a, oracle.normal(200000, 0)) and not np.array_equal(a, oracle.normal(200000, 1))
+    assert abs(a.mean()) < 0.01 and abs(a.std() - 1) < 0.01
+    t = oracle.student_t4(200000, 3)
+    # Student-t nu=4: variance nu/(nu-2) = 2
+    assert abs(t.mean()) < 0.02 and abs(t.var() - 2) < 0.2
