@@ -174,21 +174,40 @@ __global__ __launch_bounds__(256, 2) void decode_int8_kernel(DecodeParams p) {
     float m = -INFINITY, l = 0.0f;
 
     for (uint32_t t0 = begin + wave * kDecodeBlock; t0 < end; t0 += kDecodeWaves * kDecodeBlock) {
-        // ---- scores: two 16-token tiles; tile a row i holds token t0 + 8*(i/4) + 4*a + i%4,
-        // so after the MFMA lane group qq owns tokens t0 + 8*qq + [0, 8).
-        floatx4 s[2];
+        // ---- issue this block's K and V loads together (one memory round trip).
+        // K tile a row i holds token t0 + 8*(i/4) + 4*a + i%4, so after the QK MFMA
+        // lane group qq owns tokens t0 + 8*qq + [0, 8), the k-group of the PV MFMA.
+        uint4 kw[2][4];
 #pragma unroll
         for (int a = 0; a < 2; a++) {
             const uint32_t i = lane & 15;
-            uint32_t t = t0 + 8 * (i >> 2) + 4 * a + (i & 3);
-            t = min(t, length - 1);                          // loads stay inside the cache
+            const uint32_t t = min(t0 + 8 * (i >> 2) + 4 * a + (i & 3), length - 1);   // loads stay inside the cache
             const int8_t *kr = p.k + ((size_t)t * 2 + g) * 256 + 16 * qq;
+#pragma unroll
+            for (int j = 0; j < 4; j++) kw[a][j] = *reinterpret_cast<const uint4 *>(kr + 64 * j);
+        }
+        // V^T rows d = 16*dt + n, tokens t0 + 8*qq + [0, 8) (8-aligned, inside the cache)
+        const uint32_t tv = min(t0 + 8 * qq, length - 1) & ~7u;
+        const int8_t *vbase = p.v + value_index((uint64_t)tv * 2 + g, 0) + (size_t)n * 256;
+        uint2 vw[16];
+#pragma unroll
+        for (int dt = 0; dt < 16; dt++) vw[dt] = *reinterpret_cast<const uint2 *>(vbase + (size_t)dt * 16 * 256);
+        float ksc[8], vsc[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const uint32_t t = min(t0 + 8 * qq + e, length - 1);
+            ksc[e] = p.ks[(size_t)t * 2 + g];
+            vsc[e] = p.vs[(size_t)t * 2 + g];
+        }
+        // ---- scores: S^T[t][n] = K[t] . Qx[n]
+        floatx4 s[2];
+#pragma unroll
+        for (int a = 0; a < 2; a++) {
             floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const uint4 w = *reinterpret_cast<const uint4 *>(kr + 64 * j);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_half8(w.x, w.y), qop[2 * j], acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_half8(w.z, w.w), qop[2 * j + 1], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_half8(kw[a][j].x, kw[a][j].y), qop[2 * j], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_half8(kw[a][j].z, kw[a][j].w), qop[2 * j + 1], acc, 0, 0, 0);
             }
             s[a] = acc;
         }
@@ -202,7 +221,7 @@ __global__ __launch_bounds__(256, 2) void decode_int8_kernel(DecodeParams p) {
                 const float full = s[a][r] + __shfl_xor(s[a][r], 8, 64);   // hi + lo columns
                 const uint32_t t = t0 + 8 * qq + 4 * a + r;
                 float value = -INFINITY;
-                if (t < end) value = full * p.ks[(size_t)t * 2 + g] * (1.0f / 16.0f);
+                if (t < end) value = full * ksc[4 * a + r] * (1.0f / 16.0f);
                 sc[a * 4 + r] = value;
                 top = fmaxf(top, value);
             }
@@ -220,7 +239,7 @@ __global__ __launch_bounds__(256, 2) void decode_int8_kernel(DecodeParams p) {
                 const uint32_t t = t0 + 8 * qq + e + u;
                 const float prob = expf(sc[e + u] - next);          // 0 for masked tokens
                 total += prob;
-                const float scaled = t < end ? prob * p.vs[(size_t)t * 2 + g] : 0.0f;
+                const float scaled = t < end ? prob * vsc[e + u] : 0.0f;
                 const uint32_t hi = bf16_bits(scaled);
                 bits[u] = lo_col ? bf16_bits(scaled - bf16_value(hi)) : hi;
             }
@@ -235,14 +254,10 @@ __global__ __launch_bounds__(256, 2) void decode_int8_kernel(DecodeParams p) {
             for (int i = 0; i < 16; i++) o[i] *= decay;
         }
         const bf16x8 pop = __builtin_bit_cast(bf16x8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
-        // ---- values: d-tile dt, lane row d = 16*dt + n, tokens t0 + 8*qq + [0, 8)
-        const uint32_t tv = min(t0 + 8 * qq, length - 1) & ~7u;   // 8-token aligned, inside the cache
-        const int8_t *vbase = p.v + value_index((uint64_t)tv * 2 + g, 0);
+        // ---- values: O^T[d][n] += V^T[d][t] . Px[t][n], d-tile dt
 #pragma unroll
-        for (int dt = 0; dt < 16; dt++) {
-            const uint2 w = *reinterpret_cast<const uint2 *>(vbase + (size_t)(16 * dt + n) * 256);
-            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(i8x8_to_bf16x8(w.x, w.y), pop, o[dt], 0, 0, 0);
-        }
+        for (int dt = 0; dt < 16; dt++)
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(i8x8_to_bf16x8(vw[dt].x, vw[dt].y), pop, o[dt], 0, 0, 0);
     }
 
     // ---- merge the four waves: O^T[d][n] with d = 16*dt + 4*qq + r; heads sum hi + lo columns.
@@ -292,25 +307,43 @@ __global__ __launch_bounds__(256, 2) void decode_int8_kernel(DecodeParams p) {
     }
 }
 
-// Merges the splits of one (row, head) slice of 64 dims.
+// Merges the splits of one (row, head) slice of 64 dims: the split weights
+// exp(m_s - max) are computed once into LDS, then every lane streams its
+// dimension across the splits with independent loads.
+constexpr int kMaxDecodeSplits = 4096;
+
 __global__ __launch_bounds__(64) void decode_combine_kernel(const float *__restrict__ partial, const float *__restrict__ gate,
                                                             float *__restrict__ y, uint32_t splits) {
+    __shared__ float weight[kMaxDecodeSplits];
     const uint32_t row = blockIdx.z, hq = blockIdx.y, g = hq / 8, h = hq % 8;
-    const uint32_t d = blockIdx.x * 64 + threadIdx.x;
+    const int lane = threadIdx.x;
+    const uint32_t d = blockIdx.x * 64 + lane;
     const float *base = partial + ((size_t)row * 2 + g) * splits * kPartialFloats;
     float mmax = -INFINITY;
-    for (uint32_t s = 0; s < splits; s++) mmax = fmaxf(mmax, base[(size_t)s * kPartialFloats + 2048 + h]);
-    float lsum = 0.0f, osum = 0.0f;
-    for (uint32_t s = 0; s < splits; s++) {
+    for (uint32_t s = lane; s < splits; s += 64) mmax = fmaxf(mmax, base[(size_t)s * kPartialFloats + 2048 + h]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, o, 64));
+    float lsum = 0.0f;
+    for (uint32_t s = lane; s < splits; s += 64) {
         const float *part = base + (size_t)s * kPartialFloats;
         const float ms = part[2048 + h];
-        if (ms == -INFINITY) continue;
-        const float f = expf(ms - mmax);
-        lsum += part[2056 + h] * f;
-        osum += part[h * 256 + d] * f;
+        const float w = ms == -INFINITY ? 0.0f : expf(ms - mmax);
+        weight[s] = w;
+        lsum += part[2056 + h] * w;
     }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o, 64);
+    __syncthreads();
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const float *col = base + (size_t)h * 256 + d;
+    uint32_t s = 0;
+    for (; s + 4 <= splits; s += 4) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) acc[u] += col[(size_t)(s + u) * kPartialFloats] * weight[s + u];
+    }
+    for (; s < splits; s++) acc[0] += col[(size_t)s * kPartialFloats] * weight[s];
     const size_t at = ((size_t)row * 16 + hq) * 256 + d;
-    y[at] = osum / lsum * sigmoidf(gate[at]);
+    y[at] = (acc[0] + acc[1] + acc[2] + acc[3]) / lsum * sigmoidf(gate[at]);
 }
 
 inline bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
@@ -392,6 +425,7 @@ const char *launch_decode_int8(Context &c, const View *b, int count, const boot_
     uint64_t split_tokens = (length + splits - 1) / splits;
     split_tokens = std::max<uint64_t>(per_split_min, (split_tokens + per_split_min - 1) / per_split_min * per_split_min);
     splits = (length + split_tokens - 1) / split_tokens;
+    BOOT_REQUIRE(splits <= kMaxDecodeSplits, "too many decode splits");
     DecodeParams d;
     d.q = (const float *)b[0].ptr;
     d.k = (const int8_t *)b[1].ptr;

@@ -19,16 +19,20 @@
 // query layout of attention_query_grouped_half (kernels.metal:1276-1281).
 //
 // gfx950 structure (not the Metal tiling): a work-group of 4 waves owns 128
-// logical rows (16 tokens x 8 heads) of one KV group, each wave 32 rows. Per
-// 64-key step the work-group dequantizes the INT8 K tile and the V page slice
-// to FP16 once into LDS (codes are exact), then every wave computes
-// S^T = K . Q^T and O^T += V^T . P^T with v_mfma_f32_32x32x16_f16.
-// Transposed products put one query row per lane column, so row statistics are
-// per-lane and the accumulator rescale needs no cross-lane traffic; the key
-// order inside each QK tile is permuted so a lane's S registers are exactly
-// its FP16 B operand for the PV product. The exponentials run in the base-2
-// domain (the K scale carries log2(e)/16). Long histories split the key range
-// across work-groups (split-K) and a combine kernel merges (m, l, O).
+// logical rows (16 tokens x 8 heads) of one KV group, each wave 32 rows, and
+// two work-groups share a CU (two waves per SIMD) so that one work-group's MFMA
+// work overlaps the other's softmax VALU, LDS and memory latency. Per 64-key
+// step the work-group dequantizes the INT8 K tile and the V page slice to FP16
+// once into LDS (codes are exact), then every wave computes S^T = K . Q^T and
+// O^T += V^T . P^T with v_mfma_f32_32x32x16_f16. Transposed products put one
+// query row per lane column, so row statistics are per-lane and the
+// accumulator rescale needs no cross-lane traffic; the key order inside each
+// QK tile is permuted so a lane's S registers are exactly its FP16 B operand
+// for the PV product. The exponentials run in the base-2 domain (the K scale
+// carries log2(e)/16) against a lazy running maximum. Long histories split
+// the key range across work-groups (split-K) and a combine kernel merges
+// (m, l, O); blocks sharing a key range are placed on the same XCD so its L2
+// serves their K/V tiles.
 #include "common.h"
 #include "mfma.h"
 
@@ -66,6 +70,7 @@ __device__ inline float sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 // Key row of QK tile row i: bits 2 and 3 of i swapped (see header comment).
 __device__ inline int qk_key_row(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
+
 
 __global__ __launch_bounds__(256, 2) void prefill_int8_kernel(PrefillParams p) {
     __shared__ __attribute__((aligned(16))) _Float16 klds[kKeys * kKStride];
@@ -139,7 +144,7 @@ __global__ __launch_bounds__(256, 2) void prefill_int8_kernel(PrefillParams p) {
             const int krow = tid >> 2, part = tid & 3;
             const uint32_t key = min(key0 + krow, p.keys - 1);
             const uint4 *src = reinterpret_cast<const uint4 *>(p.k + ((size_t)key * 2 + g) * 256 + part * 64);
-            uint4 *dst = reinterpret_cast<uint4 *>(klds + krow * kKStride + part * 64);
+            uint4 *dst = reinterpret_cast<uint4 *>(klds + krow * kKStride);
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const uint4 w = src[j];
@@ -148,8 +153,8 @@ __global__ __launch_bounds__(256, 2) void prefill_int8_kernel(PrefillParams p) {
                 i8x4_to_f16(w.y, h[2], h[3]);
                 i8x4_to_f16(w.z, h[4], h[5]);
                 i8x4_to_f16(w.w, h[6], h[7]);
-                dst[2 * j] = make_uint4(h[0], h[1], h[2], h[3]);
-                dst[2 * j + 1] = make_uint4(h[4], h[5], h[6], h[7]);
+                dst[part * 8 + 2 * j] = make_uint4(h[0], h[1], h[2], h[3]);
+                dst[part * 8 + 2 * j + 1] = make_uint4(h[4], h[5], h[6], h[7]);
             }
         }
         // ---- stage V^T: 256 dims x 64 keys of the page slice -> FP16
@@ -184,11 +189,11 @@ __global__ __launch_bounds__(256, 2) void prefill_int8_kernel(PrefillParams p) {
             floatx16 acc;
 #pragma unroll
             for (int v = 0; v < 16; v++) acc[v] = 0.0f;
-            const _Float16 *krow = klds + (32 * a + qk_key_row(i)) * kKStride + 8 * kk;
+            const int kr = 32 * a + qk_key_row(i);
+            const half8 *krow = reinterpret_cast<const half8 *>(klds + kr * kKStride);
 #pragma unroll
             for (int c = 0; c < 16; c++)
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8 *>(krow + 16 * c), qop[c],
-                                                             acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(krow[2 * c + kk], qop[c], acc, 0, 0, 0);
             s[a] = acc;
         }
 
@@ -207,9 +212,12 @@ __global__ __launch_bounds__(256, 2) void prefill_int8_kernel(PrefillParams p) {
                 tmax = fmaxf(tmax, x);
             }
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const float mnew = fmaxf(m, tmax);
+        // lazy running maximum: rebase (and rescale the accumulator) only when a
+        // row's maximum grows by more than 2^8; exponentials stay <= 256
+        const bool rebase = tmax > m + 8.0f || (m == -INFINITY && tmax > -INFINITY);
+        const float mnew = rebase ? tmax : m;
         const float mref = mnew == -INFINITY ? 0.0f : mnew;
-        const float decay = __builtin_amdgcn_exp2f(m - mref);
+        const float decay = rebase ? (m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mnew)) : 1.0f;
         float rowsum = 0.0f;
         uint32_t pw[2][8];
 #pragma unroll

@@ -59,6 +59,9 @@ __host__ __device__ inline uint64_t value_bytes(uint64_t length) {
 const char *launch_kv_store_int8(Context &, const View *, int, const boot_kernel_args &, const uint32_t *);
 const char *launch_batch_rope_int8(Context &, const View *, int, const boot_kernel_args &, const uint32_t *);
 const char *launch_query_grouped_half(Context &, const View *, int, const boot_kernel_args &, const uint32_t *);
+const char *launch_prepare_fused_int8(Context &, const View *, int, const boot_kernel_args &, const uint32_t *);
+const char *launch_rmsnorm(Context &, const View *, int, const boot_kernel_args &, const uint32_t *);
+const char *launch_batch_split_q(Context &, const View *, int, const boot_kernel_args &, const uint32_t *);
 const char *launch_online_int8(Context &, const View *, int, const boot_kernel_args &, const uint32_t *);
 const char *launch_decode_int8(Context &, const View *, int, const boot_kernel_args &, const uint32_t *);
 const char *launch_scores_int8(Context &, const View *, int, const boot_kernel_args &, const uint32_t *);

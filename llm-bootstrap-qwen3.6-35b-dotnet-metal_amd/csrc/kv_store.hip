@@ -38,11 +38,34 @@ __device__ inline uint32_t pack4(float a, float b, float c, float d) {
            ((uint32_t)(uint8_t)(int8_t)(int)c << 16) | ((uint32_t)(uint8_t)(int8_t)(int)d << 24);
 }
 
+// Rotation angles of one position for the four dims a lane holds (4*lane .. +3):
+// lane j < 32 evaluates cos/sin of position * theta^(-2j/64) once
+// (kernels.metal:122-125), and lanes fetch the pairs of their dims
+// (j = d % 32) by shuffle, so one sincos per pair serves every head.
+struct Rope4 {
+    float c[4], s[4];
+};
+
+__device__ inline Rope4 rope_angles(uint32_t position, int lane, const float *inv_freq) {
+    float cj = 1.0f, sj = 0.0f;
+    if (lane < 32) {
+        const float angle = (float)position * inv_freq[lane];
+        sincosf(angle, &sj, &cj);
+    }
+    Rope4 r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int j = (lane * 4 + i) & 31;
+        r.c[i] = __shfl(cj, j, 64);
+        r.s[i] = __shfl(sj, j, 64);
+    }
+    return r;
+}
+
 // Partial RoPE of the float4 a lane holds (dims 4*lane .. 4*lane+3) of one
-// 256-dim head vector; dims < 64 rotate in pairs (j, j+32), j = d % 32,
-// angle = position * theta^(-2j/64) (kernels.metal:122-125). The pair partner
+// 256-dim head vector; dims < 64 rotate in pairs (j, j+32). The pair partner
 // of lane l < 16 is lane l ^ 8. Every lane must call this (shuffles).
-__device__ inline float4 rope4(float4 x, int lane, uint32_t position, const float *inv_freq) {
+__device__ inline float4 rope4(float4 x, int lane, const Rope4 &r) {
     float4 p;
     p.x = __shfl_xor(x.x, 8, 64);
     p.y = __shfl_xor(x.y, 8, 64);
@@ -50,14 +73,11 @@ __device__ inline float4 rope4(float4 x, int lane, uint32_t position, const floa
     p.w = __shfl_xor(x.w, 8, 64);
     if (lane >= 16) return x;
     float in[4] = {x.x, x.y, x.z, x.w}, partner[4] = {p.x, p.y, p.z, p.w}, out[4];
-    const float fpos = (float)position;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        int d = lane * 4 + i, j = d & 31;
-        float angle = fpos * inv_freq[j];
-        float c = cosf(angle), s = sinf(angle);
-        if (d < 32) out[i] = fmaf(in[i], c, -(partner[i] * s));   // a*cos - b*sin, b = x[j+32]
-        else out[i] = fmaf(in[i], c, partner[i] * s);              // b*cos + a*sin, a = x[j]
+        const int d = lane * 4 + i;
+        if (d < 32) out[i] = fmaf(in[i], r.c[i], -(partner[i] * r.s[i]));   // a*cos - b*sin, b = x[j+32]
+        else out[i] = fmaf(in[i], r.c[i], partner[i] * r.s[i]);              // b*cos + a*sin, a = x[j]
     }
     return make_float4(out[0], out[1], out[2], out[3]);
 }
@@ -67,43 +87,86 @@ __device__ inline void fill_inv_freq(float *inv_freq, float theta) {
     if (threadIdx.x < 32) inv_freq[threadIdx.x] = powf(theta, -(float)(2 * threadIdx.x) / 64.0f);
 }
 
+// RMS normalization of one 256-dim vector held as a float4 per lane, with the
+// weights (bf16 w + 1) of QwenEngine's q_norm/k_norm (kernels.metal:51-57 with
+// flag 1): y = x * (1/sqrt(mean(x^2) + eps)) * (w + 1). The sum of squares
+// has one fixed order (lane partial, then a butterfly), shared by rmsnorm and
+// the fused preparation so both give identical bits.
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ inline float bf16_to_float(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
+
+__device__ inline float4 rms_norm4(float4 x, float eps, const uint16_t *w, int lane, float offset) {
+    const float total = wave_sum(((x.x * x.x + x.y * x.y) + x.z * x.z) + x.w * x.w);
+    const float inv = 1.0f / sqrtf(total / 256.0f + eps);
+    const uint2 wb = *reinterpret_cast<const uint2 *>(w + 4 * lane);
+    float4 y;
+    y.x = x.x * inv * (bf16_to_float(wb.x & 0xffff) + offset);
+    y.y = x.y * inv * (bf16_to_float(wb.x >> 16) + offset);
+    y.z = x.z * inv * (bf16_to_float(wb.y & 0xffff) + offset);
+    y.w = x.w * inv * (bf16_to_float(wb.y >> 16) + offset);
+    return y;
+}
+
+struct KNorm {
+    const uint16_t *w;   // k_norm weights (bf16); null: no normalization
+    float eps;
+};
+
 // Quantizes and appends tokens [lo, hi) of one 64-token tile for one KV head.
 // K: one wave per token, float4 per lane, codes written token-major as char4.
 // V: codes transposed in LDS, then written as page rows (16-byte stores for a
 // full tile, byte stores at partial tile edges), kernels.metal:126-128.
-template <bool Rope>
+template <bool Rope, bool Norm = false>
 __device__ void store_tile(const float *__restrict__ k, const float *__restrict__ v,
                            int8_t *__restrict__ kc, int8_t *__restrict__ vc,
                            float *__restrict__ ks, float *__restrict__ vs,
                            uint32_t rows, uint32_t pos, uint32_t tile, uint32_t h,
-                           uint8_t *vt, const float *inv_freq) {
+                           uint8_t *vt, const float *inv_freq, KNorm knorm = {nullptr, 0.0f}) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t tile0 = tile * kTile;
     const uint32_t lo = max(tile0, pos), hi = min(tile0 + kTile, pos + rows);
-    for (uint32_t tl = wave; tl < kTile; tl += 4) {
-        const uint32_t t = tile0 + tl;
-        if (t < lo || t >= hi) continue;  // wave-uniform
-        const uint32_t row = t - pos;
-        const float *kr = k + ((size_t)row * 2 + h) * 256;
-        const float *vr = v + ((size_t)row * 2 + h) * 256;
-        float4 kx = *reinterpret_cast<const float4 *>(kr + 4 * lane);
-        float vx0 = vr[lane], vx1 = vr[lane + 64], vx2 = vr[lane + 128], vx3 = vr[lane + 192];
-        if (Rope) kx = rope4(kx, lane, t, inv_freq);
-        float ka = wave_max(fmaxf(fmaxf(fabsf(kx.x), fabsf(kx.y)), fmaxf(fabsf(kx.z), fabsf(kx.w))));
-        float va = wave_max(fmaxf(fmaxf(fabsf(vx0), fabsf(vx1)), fmaxf(fabsf(vx2), fabsf(vx3))));
-        const uint64_t vector = (uint64_t)t * 2 + h;
-        if (lane == 0) {
-            ks[vector] = ka / 127.0f;
-            vs[vector] = va / 127.0f;
+    // Each wave takes tokens wave, wave+4, ...; four tokens' loads are issued
+    // before any is quantized so that several requests are in flight.
+    for (uint32_t tb = wave; tb < kTile; tb += 16) {
+        float4 kx[4];
+        float vx[4][4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const uint32_t t = min(max(tile0 + tb + 4 * u, lo), hi - 1);   // in-range row for the load
+            const uint32_t row = t - pos;
+            const float *kr = k + ((size_t)row * 2 + h) * 256;
+            const float *vr = v + ((size_t)row * 2 + h) * 256;
+            kx[u] = *reinterpret_cast<const float4 *>(kr + 4 * lane);
+#pragma unroll
+            for (int i = 0; i < 4; i++) vx[u][i] = vr[lane + 64 * i];
         }
-        const float kr127 = 127.0f / ka, vr127 = 127.0f / va;
-        *reinterpret_cast<uint32_t *>(kc + vector * 256 + 4 * lane) =
-            pack4(quant_code(kx.x, ka, kr127), quant_code(kx.y, ka, kr127),
-                  quant_code(kx.z, ka, kr127), quant_code(kx.w, ka, kr127));
-        vt[(lane + 0) * kVtStride + tl] = (uint8_t)(int8_t)(int)quant_code(vx0, va, vr127);
-        vt[(lane + 64) * kVtStride + tl] = (uint8_t)(int8_t)(int)quant_code(vx1, va, vr127);
-        vt[(lane + 128) * kVtStride + tl] = (uint8_t)(int8_t)(int)quant_code(vx2, va, vr127);
-        vt[(lane + 192) * kVtStride + tl] = (uint8_t)(int8_t)(int)quant_code(vx3, va, vr127);
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const uint32_t tl = tb + 4 * u, t = tile0 + tl;
+            if (t < lo || t >= hi) continue;  // wave-uniform
+            float4 kv = kx[u];
+            if (Norm) kv = rms_norm4(kv, knorm.eps, knorm.w, lane, 1.0f);
+            if (Rope) kv = rope4(kv, lane, rope_angles(t, lane, inv_freq));
+            const float ka = wave_max(fmaxf(fmaxf(fabsf(kv.x), fabsf(kv.y)), fmaxf(fabsf(kv.z), fabsf(kv.w))));
+            const float va = wave_max(fmaxf(fmaxf(fabsf(vx[u][0]), fabsf(vx[u][1])), fmaxf(fabsf(vx[u][2]), fabsf(vx[u][3]))));
+            const uint64_t vector = (uint64_t)t * 2 + h;
+            if (lane == 0) {
+                ks[vector] = ka / 127.0f;
+                vs[vector] = va / 127.0f;
+            }
+            const float kr127 = 127.0f / ka, vr127 = 127.0f / va;
+            *reinterpret_cast<uint32_t *>(kc + vector * 256 + 4 * lane) =
+                pack4(quant_code(kv.x, ka, kr127), quant_code(kv.y, ka, kr127),
+                      quant_code(kv.z, ka, kr127), quant_code(kv.w, ka, kr127));
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                vt[(lane + 64 * i) * kVtStride + tl] = (uint8_t)(int8_t)(int)quant_code(vx[u][i], va, vr127);
+        }
     }
     __syncthreads();
     const uint64_t base = ((uint64_t)(tile0 >> 8) * 2 + h) * kPageBytes + (tile0 & 255);
@@ -145,17 +208,90 @@ __global__ __launch_bounds__(256) void batch_rope_int8_kernel(
     fill_inv_freq(inv_freq, theta);
     __syncthreads();
     if (blockIdx.x < qblocks) {
+        // one wave per row: the angles are computed once and reused by its 16 heads
         const int lane = threadIdx.x & 63;
-        const uint32_t vec = blockIdx.x * 4 + (threadIdx.x >> 6);   // row*16 + head
-        if (vec >= rows * 16) return;                                // wave-uniform
-        const uint32_t row = vec / 16;
-        float4 x = *reinterpret_cast<const float4 *>(q + (size_t)vec * 256 + 4 * lane);
-        x = rope4(x, lane, pos + row, inv_freq);
-        *reinterpret_cast<float4 *>(qr + (size_t)vec * 256 + 4 * lane) = x;
+        const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+        if (row >= rows) return;                                     // wave-uniform
+        const Rope4 r = rope_angles(pos + row, lane, inv_freq);
+        const float *src = q + (size_t)row * 4096 + 4 * lane;
+        float *dst = qr + (size_t)row * 4096 + 4 * lane;
+        float4 x[16];
+#pragma unroll
+        for (int h = 0; h < 16; h++) x[h] = *reinterpret_cast<const float4 *>(src + h * 256);
+#pragma unroll
+        for (int h = 0; h < 16; h++) *reinterpret_cast<float4 *>(dst + h * 256) = rope4(x[h], lane, r);
         return;
     }
     const uint32_t b = blockIdx.x - qblocks;
     store_tile<true>(k, v, kc, vc, ks, vs, rows, pos, first_tile + b / 2, b & 1, vt, inv_freq);
+}
+
+// attention_prepare_fused_int8 (kernels.metal:1902-1914): per row, the 16
+// query heads (RMS norm with q_norm, RoPE, FP16 into the grouped layout, gate
+// split) and the 2 KV heads (RMS norm with k_norm, RoPE, INT8 append). One wave
+// per row rotates its 16 query heads with one set of angles; K/V use the
+// page-tiled store. q holds [rows][16][q 256 | gate 256] (kernels.metal:1904).
+__global__ __launch_bounds__(256) void prepare_fused_int8_kernel(
+    const float *__restrict__ qkv, const float *__restrict__ k, const float *__restrict__ v,
+    const uint16_t *__restrict__ qw, const uint16_t *__restrict__ kw, _Float16 *__restrict__ packed,
+    float *__restrict__ gate, int8_t *__restrict__ kc, int8_t *__restrict__ vc, float *__restrict__ ks,
+    float *__restrict__ vs, uint32_t rows, uint32_t pos, float theta, float eps, uint32_t qblocks,
+    uint32_t first_tile) {
+    __shared__ __attribute__((aligned(16))) uint8_t vt[256 * kVtStride];
+    __shared__ float inv_freq[32];
+    fill_inv_freq(inv_freq, theta);
+    __syncthreads();
+    if (blockIdx.x < qblocks) {
+        const int lane = threadIdx.x & 63;
+        const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+        if (row >= rows) return;                                     // wave-uniform
+        const Rope4 r = rope_angles(pos + row, lane, inv_freq);
+        typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+#pragma unroll 4
+        for (int h = 0; h < 16; h++) {
+            const float *src = qkv + (size_t)row * 8192 + h * 512 + 4 * lane;
+            const float4 x = *reinterpret_cast<const float4 *>(src);
+            const float4 gv = *reinterpret_cast<const float4 *>(src + 256);
+            const float4 z = rope4(rms_norm4(x, eps, qw, lane, 1.0f), lane, r);
+            const half4 hz = {(_Float16)z.x, (_Float16)z.y, (_Float16)z.z, (_Float16)z.w};
+            *reinterpret_cast<half4 *>(packed + (((size_t)(h / 8) * rows + row) * 8 + h % 8) * 256 + 4 * lane) = hz;
+            *reinterpret_cast<float4 *>(gate + ((size_t)row * 16 + h) * 256 + 4 * lane) = gv;
+        }
+        return;
+    }
+    const uint32_t b = blockIdx.x - qblocks;
+    store_tile<true, true>(k, v, kc, vc, ks, vs, rows, pos, first_tile + b / 2, b & 1, vt, inv_freq, KNorm{kw, eps});
+}
+
+// rmsnorm (kernels.metal:51-57) for 256-wide groups, one wave per group:
+// y = x * rsqrt-mean-square * (w + offset) [* silu(gate) with flag 2].
+__global__ __launch_bounds__(256) void rmsnorm256_kernel(const float *__restrict__ x, const uint16_t *__restrict__ w,
+                                                         float *__restrict__ y, const float *__restrict__ gate,
+                                                         uint32_t groups, float eps, uint32_t flags) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t group = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (group >= groups) return;
+    const size_t at = (size_t)group * 256 + 4 * lane;
+    float4 z = rms_norm4(*reinterpret_cast<const float4 *>(x + at), eps, w, lane, (flags & 1) ? 1.0f : 0.0f);
+    if (flags & 2) {
+        const float4 gv = *reinterpret_cast<const float4 *>(gate + at);
+        z.x *= gv.x / (1.0f + expf(-gv.x));
+        z.y *= gv.y / (1.0f + expf(-gv.y));
+        z.z *= gv.z / (1.0f + expf(-gv.z));
+        z.w *= gv.w / (1.0f + expf(-gv.w));
+    }
+    *reinterpret_cast<float4 *>(y + at) = z;
+}
+
+// batch_split_q (kernels.metal:321): [rows][16][q | gate] -> q [rows][16][256], gate [rows][16][256].
+__global__ __launch_bounds__(256) void batch_split_q_kernel(const float *__restrict__ x, float *__restrict__ q,
+                                                            float *__restrict__ gate, uint32_t rows) {
+    const uint64_t i = ((uint64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= (uint64_t)rows * 4096) return;
+    const uint64_t token = i / 4096, h = (i % 4096) / 256, d = i % 256;
+    const float *src = x + token * 8192 + h * 512 + d;
+    *reinterpret_cast<float4 *>(q + i) = *reinterpret_cast<const float4 *>(src);
+    *reinterpret_cast<float4 *>(gate + i) = *reinterpret_cast<const float4 *>(src + 256);
 }
 
 __global__ __launch_bounds__(256) void query_grouped_half_kernel(const float *__restrict__ x,
@@ -225,7 +361,7 @@ const char *launch_batch_rope_int8(Context &c, const View *b, int count, const b
     BOOT_REQUIRE(aligned(b[0].ptr, 16) && aligned(b[1].ptr, 16) && aligned(b[2].ptr, 16) && aligned(b[3].ptr, 16),
                  "Q/K/V bindings must be 16-byte aligned");
     if (const char *e = check_cache(b, 4, 5, 6, 7, end)) return e;
-    const uint32_t qblocks = (uint32_t)((rows * 16 + 3) / 4);
+    const uint32_t qblocks = (uint32_t)((rows + 3) / 4);
     const uint32_t first = p.pos / kTile, last = (uint32_t)((end - 1) / kTile);
     const uint32_t blocks = qblocks + (last - first + 1) * 2;
     batch_rope_int8_kernel<<<blocks, 256, 0, context_stream(c)>>>(
@@ -247,6 +383,61 @@ const char *launch_query_grouped_half(Context &c, const View *b, int count, cons
     const uint64_t threads = rows * 1024;
     query_grouped_half_kernel<<<(uint32_t)((threads + 255) / 256), 256, 0, context_stream(c)>>>(
         (const float *)b[0].ptr, (_Float16 *)b[1].ptr, (uint32_t)rows, p.a);
+    return nullptr;
+}
+
+const char *launch_prepare_fused_int8(Context &c, const View *b, int count, const boot_kernel_args &p,
+                                      const uint32_t *) {
+    // bindings (Prefill.cs:250): qkv, k, v, q_norm w, k_norm w, packed Q, gate, kc, vc, ks, vs
+    BOOT_REQUIRE(count >= 11, "attention_prepare_fused_int8 needs 11 bindings");
+    const uint64_t rows = p.m, end = (uint64_t)p.pos + rows;
+    if (rows == 0) return nullptr;
+    BOOT_REQUIRE(b[0].bytes >= rows * 32768, "qkv input smaller than rows*8192 floats");
+    BOOT_REQUIRE(b[1].bytes >= rows * 2048 && b[2].bytes >= rows * 2048, "K/V input smaller than rows*512 floats");
+    BOOT_REQUIRE(b[3].bytes >= 512 && b[4].bytes >= 512, "norm weights smaller than 256 bf16");
+    BOOT_REQUIRE(b[5].bytes >= rows * 8192, "packed query smaller than rows*4096 halves");
+    BOOT_REQUIRE(b[6].bytes >= rows * 16384, "gate output smaller than rows*4096 floats");
+    BOOT_REQUIRE(aligned(b[0].ptr, 16) && aligned(b[1].ptr, 16) && aligned(b[2].ptr, 16) && aligned(b[3].ptr, 8) &&
+                     aligned(b[4].ptr, 8) && aligned(b[5].ptr, 8) && aligned(b[6].ptr, 16),
+                 "bindings misaligned");
+    if (const char *e = check_cache(b, 7, 8, 9, 10, end)) return e;
+    const uint32_t qblocks = (uint32_t)((rows + 3) / 4);
+    const uint32_t first = p.pos / kTile, last = (uint32_t)((end - 1) / kTile);
+    prepare_fused_int8_kernel<<<qblocks + (last - first + 1) * 2, 256, 0, context_stream(c)>>>(
+        (const float *)b[0].ptr, (const float *)b[1].ptr, (const float *)b[2].ptr, (const uint16_t *)b[3].ptr,
+        (const uint16_t *)b[4].ptr, (_Float16 *)b[5].ptr, (float *)b[6].ptr, (int8_t *)b[7].ptr, (int8_t *)b[8].ptr,
+        (float *)b[9].ptr, (float *)b[10].ptr, (uint32_t)rows, p.pos, p.theta, p.eps, qblocks, first);
+    return nullptr;
+}
+
+const char *launch_rmsnorm(Context &c, const View *b, int count, const boot_kernel_args &p, const uint32_t *) {
+    // bindings (QwenEngine.cs:119): x, w (bf16), y, gate; N = 256, M groups, Epsilon, Flags (1: w+1, 2: silu gate)
+    BOOT_REQUIRE(count >= 4, "rmsnorm needs 4 bindings: x, w, y, gate");
+    BOOT_REQUIRE(p.n == 256, "rmsnorm serves the 256-wide head norms of the attention path");
+    const uint64_t groups = p.m;
+    if (groups == 0) return nullptr;
+    BOOT_REQUIRE(b[0].bytes >= groups * 1024 && b[2].bytes >= groups * 1024, "x/y smaller than M*256 floats");
+    BOOT_REQUIRE(b[1].bytes >= 512, "weights smaller than 256 bf16");
+    BOOT_REQUIRE(!(p.flags & 2) || b[3].bytes >= groups * 1024, "gate smaller than M*256 floats");
+    BOOT_REQUIRE(aligned(b[0].ptr, 16) && aligned(b[1].ptr, 8) && aligned(b[2].ptr, 16) && aligned(b[3].ptr, 16),
+                 "bindings misaligned");
+    rmsnorm256_kernel<<<(uint32_t)((groups + 3) / 4), 256, 0, context_stream(c)>>>(
+        (const float *)b[0].ptr, (const uint16_t *)b[1].ptr, (float *)b[2].ptr, (const float *)b[3].ptr,
+        (uint32_t)groups, p.eps, p.flags);
+    return nullptr;
+}
+
+const char *launch_batch_split_q(Context &c, const View *b, int count, const boot_kernel_args &p, const uint32_t *) {
+    // bindings (Prefill.cs:255): x [rows][8192], q [rows][4096], gate [rows][4096]
+    BOOT_REQUIRE(count >= 3, "batch_split_q needs 3 bindings: x, q, gate");
+    const uint64_t rows = p.m;
+    if (rows == 0) return nullptr;
+    BOOT_REQUIRE(b[0].bytes >= rows * 32768 && b[1].bytes >= rows * 16384 && b[2].bytes >= rows * 16384,
+                 "buffers smaller than the split");
+    BOOT_REQUIRE(aligned(b[0].ptr, 16) && aligned(b[1].ptr, 16) && aligned(b[2].ptr, 16), "bindings misaligned");
+    const uint64_t threads = rows * 1024;
+    batch_split_q_kernel<<<(uint32_t)((threads + 255) / 256), 256, 0, context_stream(c)>>>(
+        (const float *)b[0].ptr, (float *)b[1].ptr, (float *)b[2].ptr, (uint32_t)rows);
     return nullptr;
 }
 

@@ -108,6 +108,9 @@ const std::unordered_map<std::string, Entry> &registry() {
         {"kv_store_int8", {launch_kv_store_int8, -1}},
         {"batch_rope_int8", {launch_batch_rope_int8, -1}},
         {"attention_query_grouped_half", {launch_query_grouped_half, -1}},
+        {"attention_prepare_fused_int8", {launch_prepare_fused_int8, -1}},
+        {"rmsnorm", {launch_rmsnorm, -1}},
+        {"batch_split_q", {launch_batch_split_q, -1}},
         {"attention_online_int8_q32_k256_r2", {launch_online_int8, 3}},
         {"attention_online_int8", {launch_online_int8, 3}},
         {"attention_online_int8_q32_k128", {launch_online_int8, 3}},
