@@ -115,9 +115,14 @@ __global__ __launch_bounds__(256) void values_int8_kernel(const float *__restric
 
 // ---------------------------------------------------------------- fused split-K decode
 
-constexpr int kDecodeBlock = 32;       // tokens per wave iteration
+constexpr int kDecodeBlock = 32;                 // tokens per MFMA block
+constexpr int kWaveBlocks = 4;                   // blocks per wave (128 tokens)
+constexpr int kWaveTokens = kDecodeBlock * kWaveBlocks;
 constexpr int kDecodeWaves = 4;
-constexpr int kPartialFloats = 8 * 256 + 16;   // O[8][256], m[8], l[8] per (row, group, split)
+constexpr int kSplitTokens = kDecodeWaves * kWaveTokens;   // 512 tokens per work-group
+constexpr int kPartialFloats = 8 * 256 + 16;    // O[8][256], m[8], l[8] per (row, group, split)
+constexpr int kMaxDecodeSplits = 1024;
+constexpr float kLog2e = 1.4426950408889634f;
 
 struct DecodeParams {
     const float *q;
@@ -128,90 +133,127 @@ struct DecodeParams {
     const float *gate;
     float *y;
     float *partial;
-    uint32_t rows, pos, splits, split_tokens;
+    uint32_t rows, pos, splits;
 };
 
 __device__ inline float sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-// Grid: (splits, 2 KV groups, rows). Each wave walks 32-token blocks of the
-// split; per block it computes S^T[t][n] = K[t] . Qx[n] (16x16x32 FP16 MFMA,
-// n = 8 heads x {hi, lo}), the online softmax for its 8 heads, and
-// O^T[d][n] += V^T[d][t] . Px[t][n] (16x16x32 BF16 MFMA). Lane l holds MFMA
-// column n = l % 16 and token/k group qq = l / 16.
+struct DecodeBlock {
+    uint4 k[2][4];    // K tiles a = 0, 1: 16 codes at dims 16*qq + 64*j of this lane's token
+    uint2 v[16];      // V^T rows d = 16*dt + n: 8 codes of tokens t0 + 8*qq + [0, 8)
+};
+
+// K tile a row i holds token t0 + 8*(i/4) + 4*a + i%4, so after the QK MFMA lane
+// group qq owns tokens t0 + 8*qq + [0, 8), the k-group of the PV MFMA. Addresses
+// are clamped inside the cache; tokens at or beyond the split end are masked.
+__device__ inline void load_block(DecodeBlock &blk, const DecodeParams &p, uint32_t g, uint32_t t0, uint32_t length,
+                                  int lane, int n, int qq) {
+#pragma unroll
+    for (int a = 0; a < 2; a++) {
+        const uint32_t i = lane & 15;
+        const uint32_t t = min(t0 + 8 * (i >> 2) + 4 * a + (i & 3), length - 1);
+        const int8_t *kr = p.k + ((size_t)t * 2 + g) * 256 + 16 * qq;
+#pragma unroll
+        for (int j = 0; j < 4; j++) blk.k[a][j] = *reinterpret_cast<const uint4 *>(kr + 64 * j);
+    }
+    const uint32_t tv = min(t0 + 8 * qq, length - 1) & ~7u;
+    const int8_t *vbase = p.v + value_index((uint64_t)tv * 2 + g, 0) + (size_t)n * 256;
+#pragma unroll
+    for (int dt = 0; dt < 16; dt++) blk.v[dt] = *reinterpret_cast<const uint2 *>(vbase + (size_t)dt * 16 * 256);
+}
+
+// Grid: (splits of 512 tokens, 2 KV groups, rows); 4 waves x 4 blocks of 32
+// tokens, two work-groups per CU. Each wave walks its blocks with the loads of
+// the next block in flight while the current one is computed. Per block:
+// S^T[t][n] = K[t] . Qx[n] (16x16x32 FP16 MFMA, n = 8 heads x {hi, lo}; the
+// query operands, identical for the four waves, are read from LDS), the online
+// softmax of the 8 heads in base 2, and O^T[d][n] += V^T[d][t] . Px[t][n]
+// (16x16x32 FP16 MFMA) with Px = p * vs / vs_ref split into FP16 hi + lo; vs_ref,
+// the split's largest V scale, keeps Px in [0, 1] and multiplies the result once.
+// Lane l holds MFMA column n = l % 16 and token/k group qq = l / 16.
 __global__ __launch_bounds__(256, 2) void decode_int8_kernel(DecodeParams p) {
     __shared__ float merge_o[kDecodeWaves][8][256];
     __shared__ float merge_m[kDecodeWaves][8], merge_l[kDecodeWaves][8];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __shared__ float kscale[kSplitTokens], vscale[kSplitTokens];
+    __shared__ __attribute__((aligned(16))) _Float16 qlds[8][64][8];   // [MFMA c][lane][8 dims]
+    __shared__ float red[kDecodeWaves];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, qq = lane >> 4, head = n & 7;
     const bool lo_col = n >= 8;
     const uint32_t split = blockIdx.x, g = blockIdx.y, row = blockIdx.z;
     const uint32_t length = p.pos + row + 1;
-    const uint32_t begin = split * p.split_tokens;
-    const uint32_t end = min(length, begin + p.split_tokens);
+    const uint32_t begin = split * kSplitTokens;
+    const uint32_t end = min(length, begin + kSplitTokens);
+    // Wave w takes blocks w, w+4, w+8, w+12 of the split: the four waves consume each
+    // 128-byte V page-row line (128 tokens) together, so lines are fetched once.
+    const uint32_t first = begin + wave * kDecodeBlock;
 
-    // Q^T operands: MFMA c covers dims d(c, qq, e) = 64*(c/2) + 16*qq + 8*(c%2) + e,
-    // matching the 16-byte K loads below.
-    half8 qop[8];
+    DecodeBlock cur, nxt;
+    if (first < end) load_block(cur, p, g, first, length, lane, n, qq);
+
+    // ---- scales of the split (this group) into LDS, vs_ref = their maximum
+    float vmax = 0.0f;
+    for (int e = tid; e < kSplitTokens; e += 256) {
+        const uint32_t t = begin + e;
+        const bool inside = t < end;
+        const float ksv = inside ? p.ks[(size_t)t * 2 + g] : 0.0f;
+        const float vsv = inside ? p.vs[(size_t)t * 2 + g] : 0.0f;
+        kscale[e] = ksv * (kLog2e / 16.0f);
+        vscale[e] = vsv;
+        vmax = fmaxf(vmax, vsv);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) vmax = fmaxf(vmax, __shfl_xor(vmax, o, 64));
+    if (lane == 0) red[wave] = vmax;
+    // ---- query operands, built once per work-group: MFMA c covers dims
+    // d(c, qq, e) = 64*(c/2) + 16*qq + 8*(c%2) + e, matching the 16-byte K loads
     {
+        const int c = wave * 2;   // each wave builds two of the eight operands
         const float *qh = p.q + ((size_t)row * 16 + g * 8 + head) * 256;
 #pragma unroll
-        for (int c = 0; c < 8; c++) {
-            const float *src = qh + 64 * (c >> 1) + 16 * qq + 8 * (c & 1);
-            const float4 a = *reinterpret_cast<const float4 *>(src);
-            const float4 b = *reinterpret_cast<const float4 *>(src + 4);
-            const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        for (int cc = 0; cc < 2; cc++) {
+            const float *src = qh + 64 * ((c + cc) >> 1) + 16 * qq + 8 * ((c + cc) & 1);
+            const float4 x0 = *reinterpret_cast<const float4 *>(src);
+            const float4 x1 = *reinterpret_cast<const float4 *>(src + 4);
+            const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            half8 op;
 #pragma unroll
             for (int e = 0; e < 8; e++) {
                 const _Float16 hi = (_Float16)x[e];
-                qop[c][e] = lo_col ? (_Float16)(x[e] - (float)hi) : hi;
+                op[e] = lo_col ? (_Float16)(x[e] - (float)hi) : hi;
             }
+            *reinterpret_cast<half8 *>(&qlds[c + cc][lane][0]) = op;
         }
     }
+    __syncthreads();
+    const float vs_ref = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float vs_inv = vs_ref > 0.0f ? 1.0f / vs_ref : 0.0f;
 
     floatx4 o[16];
 #pragma unroll
     for (int i = 0; i < 16; i++) o[i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     float m = -INFINITY, l = 0.0f;
 
-    for (uint32_t t0 = begin + wave * kDecodeBlock; t0 < end; t0 += kDecodeWaves * kDecodeBlock) {
-        // ---- issue this block's K and V loads together (one memory round trip).
-        // K tile a row i holds token t0 + 8*(i/4) + 4*a + i%4, so after the QK MFMA
-        // lane group qq owns tokens t0 + 8*qq + [0, 8), the k-group of the PV MFMA.
-        uint4 kw[2][4];
-#pragma unroll
-        for (int a = 0; a < 2; a++) {
-            const uint32_t i = lane & 15;
-            const uint32_t t = min(t0 + 8 * (i >> 2) + 4 * a + (i & 3), length - 1);   // loads stay inside the cache
-            const int8_t *kr = p.k + ((size_t)t * 2 + g) * 256 + 16 * qq;
-#pragma unroll
-            for (int j = 0; j < 4; j++) kw[a][j] = *reinterpret_cast<const uint4 *>(kr + 64 * j);
-        }
-        // V^T rows d = 16*dt + n, tokens t0 + 8*qq + [0, 8) (8-aligned, inside the cache)
-        const uint32_t tv = min(t0 + 8 * qq, length - 1) & ~7u;
-        const int8_t *vbase = p.v + value_index((uint64_t)tv * 2 + g, 0) + (size_t)n * 256;
-        uint2 vw[16];
-#pragma unroll
-        for (int dt = 0; dt < 16; dt++) vw[dt] = *reinterpret_cast<const uint2 *>(vbase + (size_t)dt * 16 * 256);
-        float ksc[8], vsc[8];
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const uint32_t t = min(t0 + 8 * qq + e, length - 1);
-            ksc[e] = p.ks[(size_t)t * 2 + g];
-            vsc[e] = p.vs[(size_t)t * 2 + g];
-        }
-        // ---- scores: S^T[t][n] = K[t] . Qx[n]
+    for (int b = 0; b < kWaveBlocks; b++) {
+        const uint32_t t0 = first + b * kDecodeWaves * kDecodeBlock;
+        if (t0 >= end) break;                                   // wave-uniform
+        const bool more = b + 1 < kWaveBlocks && t0 + kDecodeWaves * kDecodeBlock < end;
+        if (more) load_block(nxt, p, g, t0 + kDecodeWaves * kDecodeBlock, length, lane, n, qq);
         floatx4 s[2];
 #pragma unroll
         for (int a = 0; a < 2; a++) {
             floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_half8(kw[a][j].x, kw[a][j].y), qop[2 * j], acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_half8(kw[a][j].z, kw[a][j].w), qop[2 * j + 1], acc, 0, 0, 0);
+                const half8 q0 = *reinterpret_cast<const half8 *>(&qlds[2 * j][lane][0]);
+                const half8 q1 = *reinterpret_cast<const half8 *>(&qlds[2 * j + 1][lane][0]);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_half8(cur.k[a][j].x, cur.k[a][j].y), q0, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_half8(cur.k[a][j].z, cur.k[a][j].w), q1, acc, 0, 0, 0);
             }
             s[a] = acc;
         }
         // C layout: lane (n, qq) holds rows 4*qq + r -> token t0 + 8*qq + 4*a + r.
+        const int local0 = (int)(t0 - begin) + 8 * qq;          // token offset inside the split
         float sc[8];
         float top = -INFINITY;
 #pragma unroll
@@ -220,30 +262,29 @@ __global__ __launch_bounds__(256, 2) void decode_int8_kernel(DecodeParams p) {
             for (int r = 0; r < 4; r++) {
                 const float full = s[a][r] + __shfl_xor(s[a][r], 8, 64);   // hi + lo columns
                 const uint32_t t = t0 + 8 * qq + 4 * a + r;
-                float value = -INFINITY;
-                if (t < end) value = full * ksc[4 * a + r] * (1.0f / 16.0f);
+                const float value = t < end ? full * kscale[local0 + 4 * a + r] : -INFINITY;
                 sc[a * 4 + r] = value;
                 top = fmaxf(top, value);
             }
         top = fmaxf(top, __shfl_xor(top, 16, 64));
         top = fmaxf(top, __shfl_xor(top, 32, 64));
         const float next = fmaxf(m, top);
-        const float decay = expf(m - next);
+        const float decay = __builtin_amdgcn_exp2f(m - next);
         float total = 0.0f;
         uint32_t pw[4];
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
-            uint32_t bits[2];
+            _Float16 hv[2];
 #pragma unroll
             for (int u = 0; u < 2; u++) {
-                const uint32_t t = t0 + 8 * qq + e + u;
-                const float prob = expf(sc[e + u] - next);          // 0 for masked tokens
+                const float prob = __builtin_amdgcn_exp2f(sc[e + u] - next);   // 0 for masked tokens
                 total += prob;
-                const float scaled = t < end ? prob * vsc[e + u] : 0.0f;
-                const uint32_t hi = bf16_bits(scaled);
-                bits[u] = lo_col ? bf16_bits(scaled - bf16_value(hi)) : hi;
+                const float scaled = prob * (vscale[local0 + e + u] * vs_inv);
+                const _Float16 hi = (_Float16)scaled;
+                hv[u] = lo_col ? (_Float16)(scaled - (float)hi) : hi;
             }
-            pw[e / 2] = bits[0] | (bits[1] << 16);
+            const half2v ph = {hv[0], hv[1]};
+            pw[e / 2] = __builtin_bit_cast(uint32_t, ph);
         }
         total += __shfl_xor(total, 16, 64);
         total += __shfl_xor(total, 32, 64);
@@ -253,14 +294,15 @@ __global__ __launch_bounds__(256, 2) void decode_int8_kernel(DecodeParams p) {
 #pragma unroll
             for (int i = 0; i < 16; i++) o[i] *= decay;
         }
-        const bf16x8 pop = __builtin_bit_cast(bf16x8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
-        // ---- values: O^T[d][n] += V^T[d][t] . Px[t][n], d-tile dt
+        const half8 pop = __builtin_bit_cast(half8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
 #pragma unroll
         for (int dt = 0; dt < 16; dt++)
-            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(i8x8_to_bf16x8(vw[dt].x, vw[dt].y), pop, o[dt], 0, 0, 0);
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_half8(cur.v[dt].x, cur.v[dt].y), pop, o[dt], 0, 0, 0);
+        if (more) cur = nxt;
     }
 
-    // ---- merge the four waves: O^T[d][n] with d = 16*dt + 4*qq + r; heads sum hi + lo columns.
+    // ---- merge the four waves: O^T[d][n] with d = 16*dt + 4*qq + r; heads sum hi + lo columns;
+    // statistics are in base 2, O in units of vs_ref.
     if (n < 8) {
 #pragma unroll
         for (int dt = 0; dt < 16; dt++)
@@ -285,14 +327,14 @@ __global__ __launch_bounds__(256, 2) void decode_int8_kernel(DecodeParams p) {
     for (int w = 0; w < kDecodeWaves; w++) mw = fmaxf(mw, merge_m[w][h]);
     float lw = 0.0f, f[kDecodeWaves];
     for (int w = 0; w < kDecodeWaves; w++) {
-        f[w] = merge_m[w][h] == -INFINITY ? 0.0f : expf(merge_m[w][h] - mw);
+        f[w] = merge_m[w][h] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(merge_m[w][h] - mw);
         lw += merge_l[w][h] * f[w];
     }
     float acc[8];
     for (int e = 0; e < 8; e++) {
         float sum = 0.0f;
         for (int w = 0; w < kDecodeWaves; w++) sum += merge_o[w][h][d0 + e] * f[w];
-        acc[e] = sum;
+        acc[e] = sum * vs_ref;
     }
     if (p.splits == 1) {
         const size_t at = ((size_t)row * 16 + g * 8 + h) * 256 + d0;
@@ -307,43 +349,58 @@ __global__ __launch_bounds__(256, 2) void decode_int8_kernel(DecodeParams p) {
     }
 }
 
-// Merges the splits of one (row, head) slice of 64 dims: the split weights
-// exp(m_s - max) are computed once into LDS, then every lane streams its
-// dimension across the splits with independent loads.
-constexpr int kMaxDecodeSplits = 4096;
-
-__global__ __launch_bounds__(64) void decode_combine_kernel(const float *__restrict__ partial, const float *__restrict__ gate,
-                                                            float *__restrict__ y, uint32_t splits) {
+// Merges the splits of one (row, head) slice of 16 dims. 256 threads = 16
+// split groups x 16 dims: every thread streams every 16th split with
+// independent loads, the split weights exp2(m_s - max) are computed once into
+// LDS, and the 16 group sums are added in LDS.
+__global__ __launch_bounds__(256) void decode_combine_kernel(const float *__restrict__ partial, const float *__restrict__ gate,
+                                                             float *__restrict__ y, uint32_t splits) {
     __shared__ float weight[kMaxDecodeSplits];
+    __shared__ float red[4];
+    __shared__ float sums[16][17];
     const uint32_t row = blockIdx.z, hq = blockIdx.y, g = hq / 8, h = hq % 8;
-    const int lane = threadIdx.x;
-    const uint32_t d = blockIdx.x * 64 + lane;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float *base = partial + ((size_t)row * 2 + g) * splits * kPartialFloats;
     float mmax = -INFINITY;
-    for (uint32_t s = lane; s < splits; s += 64) mmax = fmaxf(mmax, base[(size_t)s * kPartialFloats + 2048 + h]);
+    for (uint32_t s = tid; s < splits; s += 256) mmax = fmaxf(mmax, base[(size_t)s * kPartialFloats + 2048 + h]);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, o, 64));
+    if (lane == 0) red[wave] = mmax;
+    __syncthreads();
+    mmax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     float lsum = 0.0f;
-    for (uint32_t s = lane; s < splits; s += 64) {
+    for (uint32_t s = tid; s < splits; s += 256) {
         const float *part = base + (size_t)s * kPartialFloats;
         const float ms = part[2048 + h];
-        const float w = ms == -INFINITY ? 0.0f : expf(ms - mmax);
+        const float w = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - mmax);
         weight[s] = w;
         lsum += part[2056 + h] * w;
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o, 64);
     __syncthreads();
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (lane == 0) red[wave] = lsum;
+    __syncthreads();
+    lsum = (red[0] + red[1]) + (red[2] + red[3]);
+    const int grp = tid >> 4, dl = tid & 15;
+    const uint32_t d = blockIdx.x * 16 + dl;
     const float *col = base + (size_t)h * 256 + d;
-    uint32_t s = 0;
-    for (; s + 4 <= splits; s += 4) {
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    uint32_t s = grp;
+    for (; s + 48 < splits; s += 64) {
 #pragma unroll
-        for (int u = 0; u < 4; u++) acc[u] += col[(size_t)(s + u) * kPartialFloats] * weight[s + u];
+        for (int u = 0; u < 4; u++) acc[u] += col[(size_t)(s + 16 * u) * kPartialFloats] * weight[s + 16 * u];
     }
-    for (; s < splits; s++) acc[0] += col[(size_t)s * kPartialFloats] * weight[s];
-    const size_t at = ((size_t)row * 16 + hq) * 256 + d;
-    y[at] = (acc[0] + acc[1] + acc[2] + acc[3]) / lsum * sigmoidf(gate[at]);
+    for (; s < splits; s += 16) acc[0] += col[(size_t)s * kPartialFloats] * weight[s];
+    sums[grp][dl] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    __syncthreads();
+    if (tid < 16) {
+        float total = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 16; k++) total += sums[k][tid];
+        const size_t at = ((size_t)row * 16 + hq) * 256 + blockIdx.x * 16 + tid;
+        y[at] = total / lsum * sigmoidf(gate[at]);
+    }
 }
 
 inline bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
@@ -418,13 +475,8 @@ const char *launch_decode_int8(Context &c, const View *b, int count, const boot_
     BOOT_REQUIRE(aligned(b[0].ptr, 16) && aligned(b[1].ptr, 16) && aligned(b[2].ptr, 16) && aligned(b[3].ptr, 4) &&
                      aligned(b[4].ptr, 4) && aligned(b[5].ptr, 4) && aligned(b[6].ptr, 4),
                  "bindings misaligned (q, k, v need 16 bytes)");
-    // Split the longest row's keys so that about two blocks run per CU.
-    const uint32_t per_split_min = kDecodeWaves * kDecodeBlock;   // 128 tokens
-    const uint64_t target_blocks = (uint64_t)std::max(1, context_cus(c)) * 2;
-    uint64_t splits = std::max<uint64_t>(1, target_blocks / (2 * rows));
-    uint64_t split_tokens = (length + splits - 1) / splits;
-    split_tokens = std::max<uint64_t>(per_split_min, (split_tokens + per_split_min - 1) / per_split_min * per_split_min);
-    splits = (length + split_tokens - 1) / split_tokens;
+    // Work-groups of 512 tokens (4 waves x 128); rows and groups in the grid.
+    const uint64_t splits = (length + kSplitTokens - 1) / kSplitTokens;
     BOOT_REQUIRE(splits <= kMaxDecodeSplits, "too many decode splits");
     DecodeParams d;
     d.q = (const float *)b[0].ptr;
@@ -437,7 +489,6 @@ const char *launch_decode_int8(Context &c, const View *b, int count, const boot_
     d.rows = (uint32_t)rows;
     d.pos = p.pos;
     d.splits = (uint32_t)splits;
-    d.split_tokens = (uint32_t)split_tokens;
     d.partial = nullptr;
     if (splits > 1) {
         d.partial = (float *)context_workspace(c, rows * 2 * splits * kPartialFloats * sizeof(float));
@@ -446,7 +497,7 @@ const char *launch_decode_int8(Context &c, const View *b, int count, const boot_
     decode_int8_kernel<<<dim3((uint32_t)splits, 2, (uint32_t)rows), 256, 0, context_stream(c)>>>(d);
     if (splits > 1) {
         context_split(c, "attention_decode_int8.combine");
-        decode_combine_kernel<<<dim3(4, 16, (uint32_t)rows), 64, 0, context_stream(c)>>>(d.partial, d.gate, d.y,
+        decode_combine_kernel<<<dim3(16, 16, (uint32_t)rows), 256, 0, context_stream(c)>>>(d.partial, d.gate, d.y,
                                                                                         (uint32_t)splits);
     }
     return nullptr;

@@ -178,10 +178,11 @@ __device__ void store_tile(const float *__restrict__ k, const float *__restrict_
                 make_uint4(src[0], src[1], src[2], src[3]);
         }
     } else {
-        for (int item = threadIdx.x; item < 256 * kTile; item += 256) {
-            const int d = item >> 6, tl = item & 63;
-            const uint32_t t = tile0 + tl;
-            if (t >= lo && t < hi) vc[base + (uint64_t)d * 256 + tl] = vt[d * kVtStride + tl];
+        // partial tile (chunk edges, single-token decode appends): only the valid bytes
+        const uint32_t count = hi - lo, first = lo - tile0;
+        for (uint32_t item = threadIdx.x; item < 256 * count; item += 256) {
+            const uint32_t d = item / count, tl = first + item % count;
+            vc[base + (uint64_t)d * 256 + tl] = vt[d * kVtStride + tl];
         }
     }
 }
