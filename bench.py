@@ -104,6 +104,26 @@ class PrefillWorkload:
         return sum(prefill_flops(pos, min(self.chunk, self.tokens - pos)) for pos in range(0, self.tokens, self.chunk))
 
 
+class Fp16ControlWorkload:
+    """The same prompt with FP16 KV storage (config 3's side-by-side comparator): per chunk
+    batch_rope (flags 256) -> attention_query_grouped_half -> attention_online_q32_k256_s8_g8_r2."""
+
+    def __init__(self, work: PrefillWorkload):
+        self.work = work
+        self.layer = engine.Fp16KvLayer(work.device, work.tokens)
+
+    def step(self):
+        w, d = self.work, self.work.device
+        d.begin()
+        for pos in range(0, w.tokens, w.chunk):
+            rows = min(w.chunk, w.tokens - pos)
+            rot = w.rotated.at(pos * 16384)
+            engine.append_rows_fp16(d, self.layer, w.q.at(pos * 16384), w.k.at(pos * 2048), w.v.at(pos * 2048), rot,
+                                    rows, pos)
+            engine.encode_online_fp16(w.workspace, rot, self.layer, w.gate.at(pos * 16384), rot, rows, pos)
+        d.end()
+
+
 def cpu_baseline_prefill(work: PrefillWorkload, threads: int):
     """FP64 oracle over the GPU-built INT8 cache: the last chunk of config 3, extrapolated."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
@@ -242,6 +262,22 @@ def main():
                      "frac": round(achieved / MFMA_PEAK_TFLOPS, 4), "traffic": None,
                      "flops_per_layer": flops},
     }
+    control = Fp16ControlWorkload(work)
+    for _ in range(args.warmup):
+        control.step()
+    device.reset_wall_timing(all_kernels=True)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        control.step()
+    fp16_ms = (time.perf_counter() - t0) * 1000.0 / args.steps
+    kc = kernel_stats(device, ["attention_online_q32_k256_s8_g8_r2", "attention_online_fp16.combine", "batch_rope"])
+    result["fp16_kv_control"] = {
+        "ms_per_layer": round(fp16_ms, 4),
+        "attention_kernel_ms_per_layer": round(kc["attention_online_q32_k256_s8_g8_r2"][0] / args.steps, 4),
+        "combine_ms_per_layer": round(kc.get("attention_online_fp16.combine", (0.0, 0))[0] / args.steps, 4),
+        "append_ms_per_layer": round(kc["batch_rope"][0] / args.steps, 4),
+        "int8_over_fp16_time": round(wall_ms / fp16_ms, 4),
+        "kv_bytes_30k": {"int8_with_scales": 30720 * 1040, "fp16": 30720 * 2048}}
     if not args.no_decode:
         dec = DecodeWorkload(device)
         dec.run()  # warm

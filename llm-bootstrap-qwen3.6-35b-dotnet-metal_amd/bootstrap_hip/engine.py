@@ -232,6 +232,38 @@ def store_rows(device: Device, layer: Int8KvLayer, k, v, rows: int, position: in
                     k, v, layer.key, layer.value, layer.key_scale, layer.value_scale)
 
 
+class Fp16KvLayer:
+    """FP16 control cache of one layer: token-major K and V [cap][2][256] halves
+    (kernels.metal:16-21 with flags bit 256; QwenEngine.cs:61 with KvElementBytes = 2)."""
+
+    def __init__(self, device: Device, capacity: int):
+        self.key = device.allocate(capacity * 512 * 2)
+        self.value = device.allocate(capacity * 512 * 2)
+
+    def buffers(self) -> List[GpuBuffer]:
+        return [self.key, self.value]
+
+
+def append_rows_fp16(device: Device, layer: Fp16KvLayer, q, k, v, rotated, rows: int, position: int,
+                     theta: float = ROPE_THETA) -> None:
+    """Unfused FP16 append (batch_rope with KvFlags = 256, Prefill.cs:258). Inside a command."""
+    p = KernelArgs(M=rows, Position=position, K=position + rows, Theta=theta, Flags=256)
+    device.dispatch("batch_rope", p, rows * 4096, 128, q, k, v, rotated, layer.key, layer.value)
+
+
+def encode_online_fp16(workspace: "DeviceAttentionWorkspace", q, layer: Fp16KvLayer, gate, output, rows: int,
+                       position: int, prepared_query: bool = False) -> None:
+    """DeviceAttention.cs:50-63 (EncodeOnline, FP16 KV): grouped FP16 query, then the FP16 online
+    kernel. The reference routes fewer than 32 rows to its non-online path; the gfx950 online
+    kernel serves every row count. Inside a command."""
+    device = workspace.device
+    p = KernelArgs(M=rows, K=position + rows, Position=position, A=GROUP)
+    if not prepared_query:
+        device.dispatch("attention_query_grouped_half", p, rows * 1024, 128, q, workspace.packed_query)
+    device.dispatch2d("attention_online_q32_k256_s8_g8_r2", p, (rows * 8 + 31) // 32 * 256, 2, 256,
+                      workspace.packed_query, layer.key, layer.value, gate, output)
+
+
 def decode(device: Device, layer: Int8KvLayer, rotated, gate, output, position: int, rows: int = 1) -> None:
     """Fused split-K decode over keys [0, position + row] for each row. Inside a command."""
     p = KernelArgs(M=rows, K=position + rows, Position=position)

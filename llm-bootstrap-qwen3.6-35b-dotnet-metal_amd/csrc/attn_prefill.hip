@@ -49,8 +49,8 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 struct PrefillParams {
     const _Float16 *q;      // grouped FP16 [2][M][8][256]
-    const int8_t *k;        // [cap][2][256]
-    const int8_t *v;        // V pages
+    const void *k;          // INT8 [cap][2][256] codes, or FP16 [cap][2][256] (control)
+    const void *v;          // INT8 V pages, or FP16 token-major [cap][2][256] (control)
     const float *gate;      // [M][16][256]
     float *y;               // [M][16][256]
     const float *ks, *vs;   // [cap][2]
@@ -72,7 +72,12 @@ __device__ inline float sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }
 __device__ inline int qk_key_row(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
 
 
-__global__ __launch_bounds__(256, 2) void prefill_int8_kernel(PrefillParams p) {
+// kInt8: the INT8 cache (codes + FP32 per-token scales). Otherwise the FP16
+// token-major control cache of attention_online_q32_k256_s8_g8_r2
+// (kernels.metal:1356-1365): no scales, FP16 probabilities e (<= 2^8 with the lazy
+// maximum), V transposed into LDS by the staging loop.
+template <bool kInt8>
+__global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillParams p) {
     __shared__ __attribute__((aligned(16))) _Float16 klds[kKeys * kKStride];
     __shared__ __attribute__((aligned(16))) _Float16 vlds[256 * kVStride];
     __shared__ float kscale[kKeys], vscale[kKeys];
@@ -121,8 +126,9 @@ __global__ __launch_bounds__(256, 2) void prefill_int8_kernel(PrefillParams p) {
 
     // ---- vs_ref: the largest V scale over this block's keys (0 if all are 0)
     const int tid = threadIdx.x;
-    float vs_ref = 0.0f;
-    for (uint32_t key = kbeg + tid; key < kend; key += 256) vs_ref = fmaxf(vs_ref, p.vs[(size_t)key * 2 + g]);
+    float vs_ref = kInt8 ? 0.0f : 1.0f;
+    if (kInt8)
+        for (uint32_t key = kbeg + tid; key < kend; key += 256) vs_ref = fmaxf(vs_ref, p.vs[(size_t)key * 2 + g]);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) vs_ref = fmaxf(vs_ref, __shfl_xor(vs_ref, o, 64));
     if (lane == 0) vs_partial[wave] = vs_ref;
@@ -140,10 +146,26 @@ __global__ __launch_bounds__(256, 2) void prefill_int8_kernel(PrefillParams p) {
     for (uint32_t key0 = kbeg; key0 < kend; key0 += kKeys) {
         __syncthreads();   // previous tile fully consumed
         // ---- stage K: 64 keys x 256 codes -> FP16; thread: key key0 + tid/4, 64 codes
-        {
+        if (!kInt8) {
+            // FP16 control: K rows copied as they are, V rows transposed into V^T
             const int krow = tid >> 2, part = tid & 3;
             const uint32_t key = min(key0 + krow, p.keys - 1);
-            const uint4 *src = reinterpret_cast<const uint4 *>(p.k + ((size_t)key * 2 + g) * 256 + part * 64);
+            const uint4 *ksrc = reinterpret_cast<const uint4 *>((const _Float16 *)p.k + ((size_t)key * 2 + g) * 256 + part * 64);
+            uint4 *kdst = reinterpret_cast<uint4 *>(klds + krow * kKStride);
+            const _Float16 *vsrc = (const _Float16 *)p.v + ((size_t)key * 2 + g) * 256 + part * 64;
+#pragma unroll
+            for (int j = 0; j < 8; j++) kdst[part * 8 + j] = ksrc[j];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const uint4 w = *reinterpret_cast<const uint4 *>(vsrc + 8 * j);
+                const _Float16 *hv = reinterpret_cast<const _Float16 *>(&w);
+#pragma unroll
+                for (int e = 0; e < 8; e++) vlds[(part * 64 + 8 * j + e) * kVStride + krow] = hv[e];
+            }
+        } else {
+            const int krow = tid >> 2, part = tid & 3;
+            const uint32_t key = min(key0 + krow, p.keys - 1);
+            const uint4 *src = reinterpret_cast<const uint4 *>((const int8_t *)p.k + ((size_t)key * 2 + g) * 256 + part * 64);
             uint4 *dst = reinterpret_cast<uint4 *>(klds + krow * kKStride);
 #pragma unroll
             for (int j = 0; j < 4; j++) {
@@ -158,8 +180,8 @@ __global__ __launch_bounds__(256, 2) void prefill_int8_kernel(PrefillParams p) {
             }
         }
         // ---- stage V^T: 256 dims x 64 keys of the page slice -> FP16
-        {
-            const int8_t *page = p.v + value_index((uint64_t)key0 * 2 + g, 0);
+        if (kInt8) {
+            const int8_t *page = (const int8_t *)p.v + value_index((uint64_t)key0 * 2 + g, 0);
 #pragma unroll
             for (int it = 0; it < 4; it++) {
                 const int d = it * 64 + (tid >> 2), part = tid & 3;
@@ -177,8 +199,13 @@ __global__ __launch_bounds__(256, 2) void prefill_int8_kernel(PrefillParams p) {
         if (tid < kKeys) {
             const uint32_t key = key0 + tid;
             const bool inside = key < p.keys;   // poisoned tails beyond K never reach P
-            kscale[tid] = inside ? p.ks[(size_t)key * 2 + g] * (kLog2e / 16.0f) : 0.0f;
-            vscale[tid] = inside ? p.vs[(size_t)key * 2 + g] * vs_inv : 0.0f;
+            if (kInt8) {
+                kscale[tid] = inside ? p.ks[(size_t)key * 2 + g] * (kLog2e / 16.0f) : 0.0f;
+                vscale[tid] = inside ? p.vs[(size_t)key * 2 + g] * vs_inv : 0.0f;
+            } else {
+                kscale[tid] = kLog2e / 16.0f;
+                vscale[tid] = inside ? 1.0f : 0.0f;
+            }
         }
         __syncthreads();
 
@@ -319,32 +346,36 @@ inline bool aligned(const void *ptr, uintptr_t a) { return (reinterpret_cast<uin
 
 }  // namespace
 
-const char *launch_online_int8(Context &c, const View *b, int count, const boot_kernel_args &a, const uint32_t *) {
-    // bindings (DeviceAttention.cs:69): q FP16 grouped, k, v, gate, y, ks, vs; M rows, K = pos + M,
-    // Position = pos, A = 8 heads per group.
-    BOOT_REQUIRE(count >= 7, "attention_online_int8 needs 7 bindings: q, k, v, gate, y, ks, vs");
+namespace {
+
+const char *launch_prefill(Context &c, const View *b, int count, const boot_kernel_args &a, bool int8) {
     const uint64_t rows = a.m;
     if (rows == 0) return nullptr;
-    BOOT_REQUIRE(a.a == 8 || a.a == 0, "INT8 online attention groups 8 query heads per KV head (A = 8)");
+    BOOT_REQUIRE(a.a == 8 || a.a == 0, "online attention groups 8 query heads per KV head (A = 8)");
     BOOT_REQUIRE((uint64_t)a.k == (uint64_t)a.pos + rows, "K must equal Position + M");
     const uint64_t keys = a.k;
     BOOT_REQUIRE(keys <= 262144, "attended length exceeds the 262144-token window");
     BOOT_REQUIRE(b[0].bytes >= rows * 8192, "packed FP16 query smaller than rows*4096 halves");
-    BOOT_REQUIRE(b[1].bytes >= keys * 512, "K cache smaller than K tokens");
-    BOOT_REQUIRE(b[2].bytes >= value_bytes(keys), "V cache smaller than whole pages of K tokens");
+    if (int8) {
+        BOOT_REQUIRE(b[1].bytes >= keys * 512, "K cache smaller than K tokens");
+        BOOT_REQUIRE(b[2].bytes >= value_bytes(keys), "V cache smaller than whole pages of K tokens");
+        BOOT_REQUIRE(b[5].bytes >= keys * 8 && b[6].bytes >= keys * 8, "KV scale buffers smaller than K tokens");
+        BOOT_REQUIRE(aligned(b[5].ptr, 4) && aligned(b[6].ptr, 4), "scale bindings misaligned");
+    } else {
+        BOOT_REQUIRE(b[1].bytes >= keys * 1024 && b[2].bytes >= keys * 1024, "FP16 K/V cache smaller than K tokens");
+    }
     BOOT_REQUIRE(b[3].bytes >= rows * 16384 && b[4].bytes >= rows * 16384, "gate/output smaller than rows*4096 floats");
-    BOOT_REQUIRE(b[5].bytes >= keys * 8 && b[6].bytes >= keys * 8, "KV scale buffers smaller than K tokens");
     BOOT_REQUIRE(aligned(b[0].ptr, 16) && aligned(b[1].ptr, 16) && aligned(b[2].ptr, 16) && aligned(b[3].ptr, 16) &&
-                     aligned(b[4].ptr, 16) && aligned(b[5].ptr, 4) && aligned(b[6].ptr, 4),
+                     aligned(b[4].ptr, 16),
                  "bindings misaligned (q, k, v, gate, y need 16 bytes)");
     PrefillParams p;
     p.q = (const _Float16 *)b[0].ptr;
-    p.k = (const int8_t *)b[1].ptr;
-    p.v = (const int8_t *)b[2].ptr;
+    p.k = b[1].ptr;
+    p.v = b[2].ptr;
     p.gate = (const float *)b[3].ptr;
     p.y = (float *)b[4].ptr;
-    p.ks = (const float *)b[5].ptr;
-    p.vs = (const float *)b[6].ptr;
+    p.ks = int8 ? (const float *)b[5].ptr : nullptr;
+    p.vs = int8 ? (const float *)b[6].ptr : nullptr;
     p.rows = (uint32_t)rows;
     p.pos = a.pos;
     p.keys = (uint32_t)keys;
@@ -366,12 +397,30 @@ const char *launch_online_int8(Context &c, const View *b, int count, const boot_
         p.partial = (float *)context_workspace(c, base_blocks * splits * kPartialStride * sizeof(float));
         BOOT_REQUIRE(p.partial, "cannot allocate prefill split workspace");
     }
-    prefill_int8_kernel<<<(uint32_t)blocks, 256, 0, context_stream(c)>>>(p);
+    if (int8)
+        prefill_kernel<true><<<(uint32_t)blocks, 256, 0, context_stream(c)>>>(p);
+    else
+        prefill_kernel<false><<<(uint32_t)blocks, 256, 0, context_stream(c)>>>(p);
     if (splits > 1) {
-        context_split(c, "attention_online_int8.combine");
+        context_split(c, int8 ? "attention_online_int8.combine" : "attention_online_fp16.combine");
         prefill_combine_kernel<<<dim3(kRows, p.tiles, 2), 256, 0, context_stream(c)>>>(p);
     }
     return nullptr;
+}
+
+}  // namespace
+
+const char *launch_online_int8(Context &c, const View *b, int count, const boot_kernel_args &a, const uint32_t *) {
+    // bindings (DeviceAttention.cs:69): q FP16 grouped, k, v, gate, y, ks, vs; M rows, K = pos + M,
+    // Position = pos, A = 8 heads per group.
+    BOOT_REQUIRE(count >= 7, "attention_online_int8 needs 7 bindings: q, k, v, gate, y, ks, vs");
+    return launch_prefill(c, b, count, a, true);
+}
+
+const char *launch_online_fp16(Context &c, const View *b, int count, const boot_kernel_args &a, const uint32_t *) {
+    // bindings (DeviceAttention.cs:62-63): q FP16 grouped, k FP16, v FP16 (token-major), gate, y
+    BOOT_REQUIRE(count >= 5, "attention_online_q32_k256_s8_g8_r2 needs 5 bindings: q, k, v, gate, y");
+    return launch_prefill(c, b, count, a, false);
 }
 
 }  // namespace boot

@@ -264,6 +264,38 @@ __global__ __launch_bounds__(256) void prepare_fused_int8_kernel(
     store_tile<true, true>(k, v, kc, vc, ks, vs, rows, pos, first_tile + b / 2, b & 1, vt, inv_freq, KNorm{kw, eps});
 }
 
+// batch_rope with FP16 KV storage (flags bit 256; kernels.metal:16-21, 322-324):
+// rotated Q in FP32, rotated K and V rounded to FP16 into the token-major
+// [cap][2][256] control cache. One wave per row; angles computed once per row.
+__global__ __launch_bounds__(256) void batch_rope_half_kernel(const float *__restrict__ q, const float *__restrict__ k,
+                                                              const float *__restrict__ v, float *__restrict__ qr,
+                                                              _Float16 *__restrict__ kc, _Float16 *__restrict__ vc,
+                                                              uint32_t rows, uint32_t pos, float theta) {
+    __shared__ float inv_freq[32];
+    fill_inv_freq(inv_freq, theta);
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;                                         // wave-uniform
+    const Rope4 r = rope_angles(pos + row, lane, inv_freq);
+    typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+#pragma unroll 4
+    for (int h = 0; h < 16; h++) {
+        const size_t at = (size_t)row * 4096 + h * 256 + 4 * lane;
+        *reinterpret_cast<float4 *>(qr + at) = rope4(*reinterpret_cast<const float4 *>(q + at), lane, r);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const size_t src = (size_t)row * 512 + h * 256 + 4 * lane, dst = ((size_t)(pos + row) * 2 + h) * 256 + 4 * lane;
+        const float4 kz = rope4(*reinterpret_cast<const float4 *>(k + src), lane, r);
+        const float4 vz = *reinterpret_cast<const float4 *>(v + src);
+        const half4 kh = {(_Float16)kz.x, (_Float16)kz.y, (_Float16)kz.z, (_Float16)kz.w};
+        const half4 vh = {(_Float16)vz.x, (_Float16)vz.y, (_Float16)vz.z, (_Float16)vz.w};
+        *reinterpret_cast<half4 *>(kc + dst) = kh;
+        *reinterpret_cast<half4 *>(vc + dst) = vh;
+    }
+}
+
 // rmsnorm (kernels.metal:51-57) for 256-wide groups, one wave per group:
 // y = x * rsqrt-mean-square * (w + offset) [* silu(gate) with flag 2].
 __global__ __launch_bounds__(256) void rmsnorm256_kernel(const float *__restrict__ x, const uint16_t *__restrict__ w,
@@ -408,6 +440,24 @@ const char *launch_prepare_fused_int8(Context &c, const View *b, int count, cons
         (const float *)b[0].ptr, (const float *)b[1].ptr, (const float *)b[2].ptr, (const uint16_t *)b[3].ptr,
         (const uint16_t *)b[4].ptr, (_Float16 *)b[5].ptr, (float *)b[6].ptr, (int8_t *)b[7].ptr, (int8_t *)b[8].ptr,
         (float *)b[9].ptr, (float *)b[10].ptr, (uint32_t)rows, p.pos, p.theta, p.eps, qblocks, first);
+    return nullptr;
+}
+
+const char *launch_batch_rope_half(Context &c, const View *b, int count, const boot_kernel_args &p, const uint32_t *) {
+    // bindings (Prefill.cs:258 with Flags = KvFlags): q, k, v, qr, kc, vc; FP16 storage only (flags bit 256)
+    BOOT_REQUIRE(count >= 6, "batch_rope needs 6 bindings: q, k, v, qr, kc, vc");
+    BOOT_REQUIRE(p.flags & 256, "batch_rope serves the FP16 KV storage (flags bit 256); FP32 storage is not built");
+    const uint64_t rows = p.m, end = (uint64_t)p.pos + rows;
+    if (rows == 0) return nullptr;
+    BOOT_REQUIRE(b[0].bytes >= rows * 16384 && b[3].bytes >= rows * 16384, "Q/rotated buffers smaller than rows*4096 floats");
+    BOOT_REQUIRE(b[1].bytes >= rows * 2048 && b[2].bytes >= rows * 2048, "K/V input smaller than rows*512 floats");
+    BOOT_REQUIRE(b[4].bytes >= end * 1024 && b[5].bytes >= end * 1024, "FP16 KV cache smaller than position+rows");
+    BOOT_REQUIRE(aligned(b[0].ptr, 16) && aligned(b[1].ptr, 16) && aligned(b[2].ptr, 16) && aligned(b[3].ptr, 16) &&
+                     aligned(b[4].ptr, 8) && aligned(b[5].ptr, 8),
+                 "bindings misaligned");
+    batch_rope_half_kernel<<<(uint32_t)((rows + 3) / 4), 256, 0, context_stream(c)>>>(
+        (const float *)b[0].ptr, (const float *)b[1].ptr, (const float *)b[2].ptr, (float *)b[3].ptr,
+        (_Float16 *)b[4].ptr, (_Float16 *)b[5].ptr, (uint32_t)rows, p.pos, p.theta);
     return nullptr;
 }
 
