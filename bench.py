@@ -65,6 +65,18 @@ def kernel_stats(device, names):
     return out
 
 
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of ``kernel`` (read + write) from the committed rocprofv3 PMC
+    summary (FETCH_SIZE / WRITE_SIZE, scaled by a plain device copy of known size), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            entry = json.load(f)["kernels"][kernel]
+    except (OSError, KeyError, ValueError):
+        return None
+    return int(round((entry["fetch_mb"] + entry["write_mb"]) * 1e6))
+
+
 def prefill_flops(pos: int, rows: int) -> float:
     # 4 * d * H * sum over rows of visible keys (QK and PV, 2 flop per MAC)
     return 4.0 * 256 * 16 * (rows * pos + rows * (rows + 1) / 2)
@@ -259,7 +271,8 @@ def main():
                     "mfma_fraction_end_to_end": round(flops / (wall_ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4)},
         "roofline": {"bound": "mfma", "kernel": "prefill_int8_kernel (attention_online_int8_q32_k256_r2)",
                      "achieved": round(achieved, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                     "frac": round(achieved / MFMA_PEAK_TFLOPS, 4),
+                     "traffic": measured_traffic("prefill_kernel<true>"),
                      "flops_per_layer": flops},
     }
     control = Fp16ControlWorkload(work)
@@ -306,11 +319,13 @@ def main():
         result["roofline_decode"] = {
             "bound": "hbm", "kernel": "decode_int8_kernel (attention_decode_int8)",
             "achieved": round(bytes_per_step / (dec_kernel_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(bytes_per_step / (dec_kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None}
+            "frac": round(bytes_per_step / (dec_kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic("decode_int8_kernel")}
         result["roofline_append"] = {
             "bound": "hbm", "kernel": "kv_store_int8 bulk append of 131072 tokens",
             "achieved": round(bulk_bytes / (bulk * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(bulk_bytes / (bulk * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(bulk_bytes / (bulk * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic("kv_store_int8 bulk 131072"),
             "bytes": bulk_bytes, "kernel_ms": round(bulk, 4)}
     if not args.no_cpu_baseline:
         log("cpu baseline: FP64 oracle on the last chunk")

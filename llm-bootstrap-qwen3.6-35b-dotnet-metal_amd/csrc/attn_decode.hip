@@ -9,7 +9,8 @@
 //     pages from HBM once. Scores and PV run on MFMA with FP32-faithful
 //     operands: the FP32 query is split into FP16 hi + lo halves that fill the
 //     16 MFMA columns (8 heads x {hi, lo}), and the scaled probabilities
-//     p*vs[t] likewise into BF16 hi + lo. INT8 codes are dequantized exactly
+//     p*vs[t]/vs_ref (vs_ref = the largest V scale of the split, so they lie in
+//     [0, 1]) likewise into FP16 hi + lo. INT8 codes are dequantized exactly
 //     in registers; scales are applied to scores and probabilities as the
 //     reference does (score = dot * ks[t] / 16, P = p * vs[t]).
 #include "common.h"

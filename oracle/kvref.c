@@ -265,6 +265,11 @@ static uint64_t splitmix64(uint64_t *state) {
     return z ^ (z >> 31);
 }
 
+void kvref_splitmix64(uint64_t seed, uint64_t *out, int64_t count) {
+    uint64_t state = seed;
+    for (int64_t i = 0; i < count; i++) out[i] = splitmix64(&state);
+}
+
 static double uniform01(uint64_t *state) {
     return ((double)(splitmix64(state) >> 11) + 0.5) * (1.0 / 9007199254740992.0);
 }

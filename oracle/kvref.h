@@ -90,6 +90,10 @@ void kvref_attention_fp16kv_f64(const float *q, int round_q_half,
 /* Deterministic integer-hash fill. FastAttentionTests.cs:111-119 (Fill). */
 void kvref_fill_hash(float *out, int64_t count, uint32_t seed, float scale);
 
+/* Raw splitmix64 stream (Steele, Lea, Flood 2014; Vigna's splitmix64.c): state += golden
+ * gamma, then the two xor-shift-multiply rounds. Pinned by the published outputs for seed
+ * 1234567. */
+void kvref_splitmix64(uint64_t seed, uint64_t *out, int64_t count);
 /* splitmix64 -> uniform (0,1) -> Box-Muller N(0,1), as float. */
 void kvref_normal(float *out, int64_t count, uint64_t seed);
 /* Student-t nu=4: z / sqrt(chi2_4 / 4), five normals per sample. */

@@ -47,6 +47,8 @@ class Oracle:
                                                    ctypes.c_int, ctypes.c_int, _f64p, ctypes.c_int]
         lib.kvref_fill_hash.argtypes = [_f32p, ctypes.c_int64, ctypes.c_uint32, ctypes.c_float]
         lib.kvref_normal.argtypes = [_f32p, ctypes.c_int64, ctypes.c_uint64]
+        lib.kvref_splitmix64.argtypes = [ctypes.c_uint64, np.ctypeslib.ndpointer(np.uint64, flags="C_CONTIGUOUS"),
+                                         ctypes.c_int64]
         lib.kvref_student_t4.argtypes = [_f32p, ctypes.c_int64, ctypes.c_uint64]
         self.lib = lib
         self.threads = min(16, os.cpu_count() or 1)
@@ -125,6 +127,11 @@ class Oracle:
     def fill_hash(self, count: int, seed: int, scale: float) -> np.ndarray:
         out = np.zeros(count, np.float32)
         self.lib.kvref_fill_hash(out, count, seed, scale)
+        return out
+
+    def splitmix64(self, seed: int, count: int) -> np.ndarray:
+        out = np.empty(count, np.uint64)
+        self.lib.kvref_splitmix64(seed, out, count)
         return out
 
     def normal(self, count: int, seed: int) -> np.ndarray:

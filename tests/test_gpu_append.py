@@ -1,6 +1,10 @@
 """INT8 append parity on the GPU: codes and scales bit-exact against the oracle
 (kernels.metal:129-141), guards around the written range (Int8KvTests.cs:43,64-70),
 partial RoPE to tolerance (KvStorageTests.cs:44-57, Int8KvTests.cs:46-62)."""
+import hashlib
+import json
+import os
+
 import numpy as np
 import pytest
 
@@ -34,10 +38,16 @@ def assert_same_bytes(got, ref):
 
 
 def test_config1_append_512_bitexact(device, oracle):
-    """Config 1: 512 tokens of N(0,1) K/V, seed 0, at position 0."""
+    """Config 1: 512 tokens of N(0,1) K/V, seed 0, at position 0; the device cache also
+    hashes to the committed digests of tests/golden/kv_golden.json."""
     k = oracle.normal(512 * 512, 0).reshape(512, 2, 256)
     v = oracle.normal(512 * 512, 1).reshape(512, 2, 256)
-    assert_same_bytes(*run_store(device, oracle, k, v, 0, guard=0))
+    got, ref = run_store(device, oracle, k, v, 0, guard=0)
+    assert_same_bytes(got, ref)
+    with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "kv_golden.json")) as f:
+        digests = json.load(f)["config1"]["sha256"]
+    for name, a in zip(("key_codes", "value_pages", "key_scales", "value_scales"), got):
+        assert hashlib.sha256(a.tobytes()).hexdigest() == digests[name], name
 
 
 @pytest.mark.parametrize("pos,rows", [(0, 1), (17, 7), (63, 2), (255, 2), (4093, 33), (1000, 600), (4096, 512),
