@@ -319,22 +319,402 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillParams p) {
     }
 }
 
+// ---------------------------------------------------------------- INT8 prefill, two-team schedule
+//
+// A work-group of 8 waves owns 256 logical rows (32 tokens x 8 heads) of one KV
+// group and walks its key range in 32-key tiles. Waves w and w + 4 share a SIMD;
+// waves 0-3 form team 0, waves 4-7 team 1. The loop runs in slots separated by
+// work-group barriers, and in every slot one team issues its MFMAs (O^T += V^T P^T
+// for the previous tile, then S^T = K Q^T for the current one) while the other
+// team runs the VALU work (online softmax of its S and half of the INT8 -> FP16
+// staging of the next tile: team 0 converts K, team 1 the V page slice). The
+// MFMA pipe of each SIMD thus alternates between its two waves while the other
+// wave's VALU instructions issue beside it, instead of both waves waiting on the
+// same barrier with the same kind of work. Tiles live in two LDS buffers; the raw
+// codes of the tile after next are loaded into registers a full iteration ahead.
+//
+// Schedule (n = tile): slot 2n: team 0 MFMA(n), team 1 VALU(n-1);
+//                      slot 2n+1: team 0 VALU(n), team 1 MFMA(n).
+// VALU(n) of team 0 writes K, scales of tile n+1 into buffer (n+1)&1, whose tile
+// n-1 was last read in slot 2n-1; VALU(n) of team 1 (slot 2n+2) writes V of tile
+// n+1, whose buffer was last read in slot 2n+1.
+constexpr int kPPRows = 256;               // logical rows per work-group
+constexpr int kPPKeys = 32;                // keys per tile
+constexpr int kPPVStride = kPPKeys + 8;    // FP16 V^T tile row stride (halves): 80 bytes
+constexpr size_t kPPPartialStride = (size_t)kPPRows * 256 + 2 * kPPRows;
+constexpr int kPPQRegs = 6;                // Q^T operand chunks held in registers; the rest in LDS
+
+// Max and sum over the lane pair (l, l ^ 32): v_permlane32_swap leaves lanes
+// 0-31 of one result and 32-63 of the other holding the pair's two values.
+__device__ inline float pair_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                    false, false);
+    return fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
+}
+
+// v_max3_f32 without the canonicalizing moves the compiler adds in front of
+// fmaxf when it cannot prove its inputs canonical (no NaN reaches this kernel).
+__device__ inline float max3f(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
+struct PPTile {
+    _Float16 k[kPPKeys * kKStride];        // K codes as FP16, key-major
+    _Float16 v[256 * kPPVStride];          // V^T codes as FP16, dimension-major
+    float ks[kPPKeys];                     // K scale * log2(e) / 16
+    float vs[kPPKeys];                     // V scale / vs_ref
+};
+
+__global__ __launch_bounds__(512, 1) void prefill_pp_kernel(PrefillParams p) {
+    __shared__ PPTile buf[2];
+    __shared__ uint4 qlds[16 - kPPQRegs][512];   // each lane's own Q^T operands for chunks kPPQRegs..15
+    __shared__ float vs_partial[8];
+
+    uint32_t g, tile, split;
+    {
+        const uint32_t b = blockIdx.x;
+        uint32_t combo;
+        if (p.remap) {
+            const uint32_t xcd = b % 8, idx = b / 8;
+            combo = xcd + 8 * (idx / p.tiles);
+            tile = idx % p.tiles;
+        } else {
+            combo = b / p.tiles;
+            tile = b % p.tiles;
+        }
+        g = combo % 2;
+        split = combo / 2;
+    }
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int team = wave >> 2;
+    const int t = tid & 255;
+    const int i = lane & 31, kk = lane >> 5;
+    const uint32_t R = p.rows * 8;
+    const uint32_t r0 = tile * kPPRows;
+    const uint32_t my_row = r0 + 32 * wave + i;
+    const bool row_valid = my_row < R;
+    const uint32_t rr = row_valid ? my_row : R - 1;
+    const uint32_t limit = p.pos + rr / 8;                              // keys <= limit visible
+    const uint32_t tile_last = min(R - 1, r0 + kPPRows - 1);
+    const uint32_t tile_end = p.pos + tile_last / 8 + 1;               // keys [0, tile_end)
+    const uint32_t kbeg = split * p.split_keys;
+    const uint32_t kend = min(tile_end, kbeg + p.split_keys);
+    const int ntiles = kend > kbeg ? (int)((kend - kbeg + kPPKeys - 1) / kPPKeys) : 0;
+    const uint32_t wave_min_limit = p.pos + min(R - 1, r0 + 32 * wave) / 8;
+
+    // Q^T operands (B of the QK product): lane (i, kk), dims 16c + 8kk + [0, 8); the
+    // last chunks wait in LDS, each lane reading back only what it wrote
+    half8 qop[kPPQRegs];
+    {
+        const _Float16 *qrow = p.q + ((size_t)g * R + rr) * 256 + 8 * kk;
+#pragma unroll
+        for (int c = 0; c < kPPQRegs; c++) qop[c] = *reinterpret_cast<const half8 *>(qrow + 16 * c);
+#pragma unroll
+        for (int c = kPPQRegs; c < 16; c++) qlds[c - kPPQRegs][tid] = *reinterpret_cast<const uint4 *>(qrow + 16 * c);
+    }
+
+    // vs_ref: the largest V scale over this block's keys (0 if all are 0)
+    float vs_ref = 0.0f;
+    for (uint32_t key = kbeg + tid; key < kend; key += 512) vs_ref = fmaxf(vs_ref, p.vs[(size_t)key * 2 + g]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) vs_ref = fmaxf(vs_ref, __shfl_xor(vs_ref, o, 64));
+    if (lane == 0) vs_partial[wave] = vs_ref;
+    __syncthreads();
+    vs_ref = vs_partial[0];
+#pragma unroll
+    for (int w = 1; w < 8; w++) vs_ref = fmaxf(vs_ref, vs_partial[w]);
+    // work-group uniform: scalar registers
+    vs_ref = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, vs_ref)));
+    const float vs_inv = __builtin_bit_cast(
+        float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, vs_ref > 0.0f ? 1.0f / vs_ref : 0.0f)));
+
+    // Staging of the FP16 tiles. Team 0 thread t (wave t / 64 of the team, lane t % 64): K rows
+    // 8 (t / 64) + 4j + (t % 64) / 16 for j = 0, 1, 16 codes at 16 (t % 16); a load
+    // instruction reads four whole 256-byte rows. Team 1 thread t: dimension t of
+    // the V^T tile, the 32 codes of its page row. Team 0 threads t < 32 also carry
+    // the K and V scales of key t (loaded one tile ahead of their store).
+    const int8_t *kcodes = (const int8_t *)p.k;
+    const int8_t *vcodes = (const int8_t *)p.v;
+    uint4 raw0 = make_uint4(0, 0, 0, 0), raw1 = raw0;
+    float pre_ks = 0.0f, pre_vs = 0.0f;
+    const int krow0 = 8 * (t >> 6) + ((t & 63) >> 4), kchunk = t & 15;
+    auto load_raw = [&](uint32_t key0) {
+        if (team == 0) {
+            const uint32_t ka = min(key0 + (uint32_t)krow0, p.keys - 1);
+            const uint32_t kb2 = min(key0 + (uint32_t)krow0 + 4, p.keys - 1);
+            const uint32_t offa = (ka * 2 + g) * 256 + kchunk * 16, offb = (kb2 * 2 + g) * 256 + kchunk * 16;   // < 2^27
+            raw0 = *reinterpret_cast<const uint4 *>(kcodes + (size_t)offa);
+            raw1 = *reinterpret_cast<const uint4 *>(kcodes + (size_t)offb);
+        } else {
+            const uint32_t off = (uint32_t)value_index((uint64_t)key0 * 2 + g, 0) + (uint32_t)t * 256;
+            const uint4 *src = reinterpret_cast<const uint4 *>(vcodes + off);
+            raw0 = src[0];
+            raw1 = src[1];
+        }
+    };
+    auto load_scales = [&](uint32_t key0) {
+        if (team == 0 && t < kPPKeys) {
+            // raw scales; they are scaled when stored, a full iteration later, so the
+            // wave never waits for these loads here
+            const size_t at = (size_t)min(key0 + t, p.keys - 1) * 2 + g;
+            pre_ks = p.ks[at];
+            pre_vs = p.vs[at];
+        }
+    };
+    auto store_scales = [&](PPTile &b, uint32_t key0) {
+        if (team == 0 && t < kPPKeys) {
+            const bool inside = key0 + t < p.keys;   // poisoned tails beyond K never reach S or P
+            b.ks[t] = inside ? pre_ks * (kLog2e / 16.0f) : 0.0f;
+            b.vs[t] = inside ? pre_vs * vs_inv : 0.0f;
+        }
+    };
+    // quad q (0..3) of the thread's converted codes: dwords 2q, 2q + 1 of raw0, raw1
+    auto quad_dst = [&](PPTile &b, int q) {
+        return team == 0 ? reinterpret_cast<uint4 *>(b.k + (krow0 + 4 * (q >> 1)) * kKStride + kchunk * 16 + 8 * (q & 1))
+                         : reinterpret_cast<uint4 *>(b.v + t * kPPVStride + 8 * q);
+    };
+    auto convert_quad = [&](int q) {
+        const uint32_t w0 = q == 0 ? raw0.x : q == 1 ? raw0.z : q == 2 ? raw1.x : raw1.z;
+        const uint32_t w1 = q == 0 ? raw0.y : q == 1 ? raw0.w : q == 2 ? raw1.y : raw1.w;
+        uint4 h;
+        i8x4_to_f16(w0, h.x, h.y);
+        i8x4_to_f16(w1, h.z, h.w);
+        return h;
+    };
+
+    if (ntiles > 0) {
+        load_raw(kbeg);
+        load_scales(kbeg);
+#pragma unroll
+        for (int q = 0; q < 4; q++) *quad_dst(buf[0], q) = convert_quad(q);
+        store_scales(buf[0], kbeg);
+        if (ntiles > 1) {
+            load_raw(kbeg + kPPKeys);
+            load_scales(kbeg + kPPKeys);
+        }
+    }
+    __syncthreads();
+
+    floatx16 o[8];
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) o[dt][v] = 0.0f;
+    float m = -INFINITY, l = 0.0f;
+    floatx16 s;
+#pragma unroll
+    for (int v = 0; v < 16; v++) s[v] = 0.0f;
+    half8 pb[2];
+#pragma unroll
+    for (int e = 0; e < 8; e++) pb[0][e] = pb[1][e] = (_Float16)0.0f;
+
+    const int slots = 2 * ntiles + 2;
+    for (int slot = 0; slot < slots; slot++) {
+        const int phase = slot - team;
+        if (phase >= 0) {
+            const int n = phase >> 1;
+            if ((phase & 1) == 0) {
+                // ---- MFMA work: O^T += V^T(n-1) . P^T(n-1) and S^T = K(n) . Q^T. The two
+                // products are interleaved (the QK accumulation chain always has an
+                // independent PV product between its steps) and every operand is read
+                // from LDS two steps before its MFMA.
+                const _Float16 *vt = buf[(n - 1) & 1].v + i * kPPVStride + 8 * kk;
+                const _Float16 *kr = buf[n & 1].k + qk_key_row(i) * kKStride + 8 * kk;
+                auto vop = [&](int j) {   // PV step j: u = j / 8, dt = j % 8
+                    return *reinterpret_cast<const half8 *>(vt + 32 * (j & 7) * kPPVStride + 16 * (j >> 3));
+                };
+                auto kop = [&](int c) { return *reinterpret_cast<const half8 *>(kr + 16 * c); };
+                auto qop_at = [&](int c) {
+                    return c < kPPQRegs ? qop[c < kPPQRegs ? c : 0]
+                                        : __builtin_bit_cast(half8, qlds[c < kPPQRegs ? 0 : c - kPPQRegs][tid]);
+                };
+                if (n >= 1 && n < ntiles) {
+#pragma unroll
+                    for (int v = 0; v < 16; v++) s[v] = 0.0f;
+                    half8 va = vop(0), ka = kop(0), qa = qop_at(0);
+                    half8 vb = vop(1), kb = kop(1), qb = qop_at(1);
+#pragma unroll
+                    for (int j = 0; j < 16; j++) {
+                        half8 vc = va, kc = ka, qc = qa;
+                        if (j + 2 < 16) {
+                            vc = vop(j + 2);
+                            kc = kop(j + 2);
+                            qc = qop_at(j + 2);
+                        }
+                        // keep the reads of step j + 2 ahead of the MFMAs of step j
+                        __builtin_amdgcn_sched_barrier(0);
+                        o[j & 7] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[j >> 3], o[j & 7], 0, 0, 0);
+                        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qa, s, 0, 0, 0);
+                        __builtin_amdgcn_sched_barrier(0);
+                        va = vb; ka = kb; qa = qb;
+                        vb = vc; kb = kc; qb = qc;
+                    }
+                } else if (n >= 1) {
+                    half8 va = vop(0), vb = vop(1);
+#pragma unroll
+                    for (int j = 0; j < 16; j++) {
+                        half8 vc = va;
+                        if (j + 2 < 16) vc = vop(j + 2);
+                        __builtin_amdgcn_sched_barrier(0);
+                        o[j & 7] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[j >> 3], o[j & 7], 0, 0, 0);
+                        __builtin_amdgcn_sched_barrier(0);
+                        va = vb;
+                        vb = vc;
+                    }
+                } else if (n < ntiles) {
+#pragma unroll
+                    for (int v = 0; v < 16; v++) s[v] = 0.0f;
+                    half8 ka = kop(0), qa = qop_at(0), kb = kop(1), qb = qop_at(1);
+#pragma unroll
+                    for (int c = 0; c < 16; c++) {
+                        half8 kc = ka, qc = qa;
+                        if (c + 2 < 16) {
+                            kc = kop(c + 2);
+                            qc = qop_at(c + 2);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+                        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qa, s, 0, 0, 0);
+                        __builtin_amdgcn_sched_barrier(0);
+                        ka = kb; qa = qb;
+                        kb = kc; qb = qc;
+                    }
+                }
+            } else if (n < ntiles) {
+                // ---- VALU work: staging of tile n+1 and the prefetch of tile n+2 first
+                // (their registers are free again before the softmax needs its own),
+                // then the online softmax of tile n (lane value v is key
+                // key0 + 16(v/8) + 8kk + v%8)
+                const uint32_t key0 = kbeg + (uint32_t)n * kPPKeys;
+                const PPTile &b = buf[n & 1];
+                // K scales of the lane's keys first: their LDS latency overlaps the staging
+                float4 k4[4];
+#pragma unroll
+                for (int q4 = 0; q4 < 4; q4++)
+                    k4[q4] = *reinterpret_cast<const float4 *>(b.ks + 16 * (q4 >> 1) + 8 * kk + 4 * (q4 & 1));
+                if (n + 1 < ntiles) {
+                    // tile n+1: team 0 writes K and the scales (buffer last read in slot
+                    // 2n - 1, scales in slot 2n), team 1 writes V (last read in slot 2n + 1)
+                    PPTile &nb = buf[(n + 1) & 1];
+#pragma unroll
+                    for (int q = 0; q < 4; q++) *quad_dst(nb, q) = convert_quad(q);
+                    store_scales(nb, key0 + kPPKeys);
+                    if (n + 2 < ntiles) {
+                        load_raw(key0 + 2 * kPPKeys);
+                        load_scales(key0 + 2 * kPPKeys);
+                    }
+                }
+                const float mref = m == -INFINITY ? 0.0f : m;
+#pragma unroll
+                for (int q4 = 0; q4 < 4; q4++) {
+                    s[4 * q4 + 0] = fmaf(s[4 * q4 + 0], k4[q4].x, -mref);
+                    s[4 * q4 + 1] = fmaf(s[4 * q4 + 1], k4[q4].y, -mref);
+                    s[4 * q4 + 2] = fmaf(s[4 * q4 + 2], k4[q4].z, -mref);
+                    s[4 * q4 + 3] = fmaf(s[4 * q4 + 3], k4[q4].w, -mref);
+                }
+                if (key0 + kPPKeys - 1 > wave_min_limit) {
+#pragma unroll
+                    for (int v = 0; v < 16; v++)
+                        if (key0 + 16 * (v >> 3) + 8 * kk + (v & 7) > limit) s[v] = -INFINITY;
+                }
+                const float ma = max3f(s[0], s[1], s[2]), mb = max3f(s[3], s[4], s[5]), mc = max3f(s[6], s[7], s[8]);
+                const float md = max3f(s[9], s[10], s[11]), me = max3f(s[12], s[13], s[14]);
+                const float ymax = pair_max(max3f(max3f(ma, mb, mc), max3f(md, me, s[15]), s[15]));
+                // lazy running maximum: rebase (and rescale the accumulator) only when a
+                // row's maximum grows by more than 2^8; exponentials stay <= 256
+                const bool rebase = ymax > 8.0f || (m == -INFINITY && ymax > -INFINITY);
+                if (__ballot(rebase)) {
+                    float decay = 1.0f, shift = 0.0f;
+                    if (rebase) {
+                        shift = ymax;
+                        decay = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(-ymax);
+                        m = mref + ymax;
+                    }
+#pragma unroll
+                    for (int v = 0; v < 16; v++) s[v] -= shift;
+                    l *= decay;
+#pragma unroll
+                    for (int dt = 0; dt < 8; dt++) o[dt] *= decay;
+                }
+                float lsum = 0.0f;
+#pragma unroll
+                for (int q4 = 0; q4 < 4; q4++) {
+                    const float4 v4 = *reinterpret_cast<const float4 *>(b.vs + 16 * (q4 >> 1) + 8 * kk + 4 * (q4 & 1));
+                    const float e0 = __builtin_amdgcn_exp2f(s[4 * q4 + 0]);
+                    const float e1 = __builtin_amdgcn_exp2f(s[4 * q4 + 1]);
+                    const float e2 = __builtin_amdgcn_exp2f(s[4 * q4 + 2]);
+                    const float e3 = __builtin_amdgcn_exp2f(s[4 * q4 + 3]);
+                    lsum += (e0 + e1) + (e2 + e3);
+                    const int u = q4 >> 1, e = 4 * (q4 & 1);
+                    pb[u][e + 0] = (_Float16)(e0 * v4.x);        // RNE
+                    pb[u][e + 1] = (_Float16)(e1 * v4.y);
+                    pb[u][e + 2] = (_Float16)(e2 * v4.z);
+                    pb[u][e + 3] = (_Float16)(e3 * v4.w);
+                }
+                l += lsum;
+            }
+        }
+        __syncthreads();
+    }
+    l += __shfl_xor(l, 32, 64);   // the two lanes of a row summed disjoint keys
+
+    // ---- epilogue: lane (i, kk) holds O^T[d][row] for d = 32dt + 8(v/4) + 4kk + v%4
+    if (p.splits == 1) {
+        if (!row_valid) return;
+        const uint32_t token = my_row / 8, head = g * 8 + my_row % 8;
+        const size_t base = ((size_t)token * 16 + head) * 256;
+        const float inv = vs_ref / l;
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+            for (int vq = 0; vq < 4; vq++) {
+                const int d = 32 * dt + 8 * vq + 4 * kk;
+                const float4 gv = *reinterpret_cast<const float4 *>(p.gate + base + d);
+                float4 out;
+                out.x = o[dt][4 * vq + 0] * inv * sigmoidf(gv.x);
+                out.y = o[dt][4 * vq + 1] * inv * sigmoidf(gv.y);
+                out.z = o[dt][4 * vq + 2] * inv * sigmoidf(gv.z);
+                out.w = o[dt][4 * vq + 3] * inv * sigmoidf(gv.w);
+                *reinterpret_cast<float4 *>(p.y + base + d) = out;
+            }
+        return;
+    }
+    float *part = p.partial + (((size_t)g * p.tiles + tile) * p.splits + split) * kPPPartialStride;
+    const int local_row = 32 * wave + i;
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+        for (int vq = 0; vq < 4; vq++) {
+            const int d = 32 * dt + 8 * vq + 4 * kk;
+            *reinterpret_cast<float4 *>(part + (size_t)local_row * 256 + d) =
+                make_float4(o[dt][4 * vq] * vs_ref, o[dt][4 * vq + 1] * vs_ref, o[dt][4 * vq + 2] * vs_ref,
+                            o[dt][4 * vq + 3] * vs_ref);
+        }
+    if (kk == 0) {
+        part[(size_t)kPPRows * 256 + local_row] = m;
+        part[(size_t)kPPRows * 256 + kPPRows + local_row] = l;
+    }
+}
+
 // One block per (group, tile, logical row); thread d merges the splits.
+template <int kTileRows>
 __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillParams p) {
+    constexpr size_t kStride = (size_t)kTileRows * 256 + 2 * kTileRows;
     const uint32_t local_row = blockIdx.x, tile = blockIdx.y, g = blockIdx.z;
-    const uint32_t row = tile * kRows + local_row;
+    const uint32_t row = tile * kTileRows + local_row;
     if (row >= p.rows * 8) return;
-    const float *base = p.partial + ((size_t)g * p.tiles + tile) * p.splits * kPartialStride;
+    const float *base = p.partial + ((size_t)g * p.tiles + tile) * p.splits * kStride;
     float mmax = -INFINITY;
-    for (uint32_t s = 0; s < p.splits; s++) mmax = fmaxf(mmax, base[s * kPartialStride + (size_t)kRows * 256 + local_row]);
+    for (uint32_t s = 0; s < p.splits; s++) mmax = fmaxf(mmax, base[s * kStride + (size_t)kTileRows * 256 + local_row]);
     const int d = threadIdx.x;
     float lsum = 0.0f, osum = 0.0f;
     for (uint32_t s = 0; s < p.splits; s++) {
-        const float *part = base + s * kPartialStride;
-        const float ms = part[(size_t)kRows * 256 + local_row];
+        const float *part = base + s * kStride;
+        const float ms = part[(size_t)kTileRows * 256 + local_row];
         if (ms == -INFINITY) continue;
         const float f = __builtin_amdgcn_exp2f(ms - mmax);
-        lsum += part[(size_t)kRows * 256 + kRows + local_row] * f;
+        lsum += part[(size_t)kTileRows * 256 + kTileRows + local_row] * f;
         osum += part[(size_t)local_row * 256 + d] * f;
     }
     const uint32_t token = row / 8, head = g * 8 + row % 8;
@@ -379,14 +759,20 @@ const char *launch_prefill(Context &c, const View *b, int count, const boot_kern
     p.rows = (uint32_t)rows;
     p.pos = a.pos;
     p.keys = (uint32_t)keys;
-    p.tiles = (uint32_t)((rows * 8 + kRows - 1) / kRows);
-    // split-K: enough blocks for two per CU, each split at least 256 keys
+    // INT8: 256-row work-groups of 8 waves, one per CU; FP16 control: 128-row
+    // work-groups of 4 waves, two per CU.
+    const uint64_t tile_rows = int8 ? kPPRows : kRows;
+    const uint64_t tile_keys = int8 ? kPPKeys : kKeys;
+    const uint64_t per_cu = int8 ? 1 : 2;
+    const size_t stride = int8 ? kPPPartialStride : kPartialStride;
+    p.tiles = (uint32_t)((rows * 8 + tile_rows - 1) / tile_rows);
+    // split-K: enough blocks to fill the CUs, each split at least 256 keys
     const uint64_t base_blocks = 2ull * p.tiles;
-    const uint64_t want = 2ull * (uint64_t)std::max(1, context_cus(c));
+    const uint64_t want = per_cu * (uint64_t)std::max(1, context_cus(c));
     uint64_t splits = std::max<uint64_t>(1, (want + base_blocks - 1) / base_blocks);
     splits = std::min<uint64_t>(splits, std::max<uint64_t>(1, keys / 256));
     uint64_t split_keys = (keys + splits - 1) / splits;
-    split_keys = (split_keys + kKeys - 1) / kKeys * kKeys;
+    split_keys = (split_keys + tile_keys - 1) / tile_keys * tile_keys;
     splits = (keys + split_keys - 1) / split_keys;
     p.splits = (uint32_t)splits;
     p.split_keys = (uint32_t)split_keys;
@@ -394,16 +780,19 @@ const char *launch_prefill(Context &c, const View *b, int count, const boot_kern
     p.remap = ((2 * splits) % 8 == 0) ? 1u : 0u;
     p.partial = nullptr;
     if (splits > 1) {
-        p.partial = (float *)context_workspace(c, base_blocks * splits * kPartialStride * sizeof(float));
+        p.partial = (float *)context_workspace(c, base_blocks * splits * stride * sizeof(float));
         BOOT_REQUIRE(p.partial, "cannot allocate prefill split workspace");
     }
     if (int8)
-        prefill_kernel<true><<<(uint32_t)blocks, 256, 0, context_stream(c)>>>(p);
+        prefill_pp_kernel<<<(uint32_t)blocks, 512, 0, context_stream(c)>>>(p);
     else
         prefill_kernel<false><<<(uint32_t)blocks, 256, 0, context_stream(c)>>>(p);
     if (splits > 1) {
         context_split(c, int8 ? "attention_online_int8.combine" : "attention_online_fp16.combine");
-        prefill_combine_kernel<<<dim3(kRows, p.tiles, 2), 256, 0, context_stream(c)>>>(p);
+        if (int8)
+            prefill_combine_kernel<kPPRows><<<dim3(kPPRows, p.tiles, 2), 256, 0, context_stream(c)>>>(p);
+        else
+            prefill_combine_kernel<kRows><<<dim3(kRows, p.tiles, 2), 256, 0, context_stream(c)>>>(p);
     }
     return nullptr;
 }
