@@ -244,16 +244,21 @@ def main():
     work = PrefillWorkload(device)
     for _ in range(args.warmup):
         work.step()
-    device.reset_wall_timing(all_kernels=True)
+    # timed region: HIP events only around the attention kernels (the roofline's
+    # durations); each step ends with the library's stream synchronized (boot_end)
+    device.reset_wall_timing(sample_attention=True)
     t0 = time.perf_counter()
     for _ in range(args.steps):
         work.step()
     wall_ms = (time.perf_counter() - t0) * 1000.0 / args.steps
-    ks = kernel_stats(device, ["attention_online_int8_q32_k256_r2", "attention_online_int8.combine",
-                               "batch_rope_int8", "attention_query_grouped_half"])
+    ks = kernel_stats(device, ["attention_online_int8_q32_k256_r2", "attention_online_int8.combine"])
     attn_ms = ks["attention_online_int8_q32_k256_r2"][0] / args.steps
     combine_ms = ks.get("attention_online_int8.combine", (0.0, 0))[0] / args.steps
     launches = ks["attention_online_int8_q32_k256_r2"][1] // args.steps
+    # one more step with events around every kernel for the breakdown (not timed)
+    device.reset_wall_timing(all_kernels=True)
+    work.step()
+    ks.update(kernel_stats(device, ["batch_rope_int8", "attention_query_grouped_half"]))
     flops = work.flops()
     achieved = flops / (attn_ms * 1e-3) / 1e12
     result = {
@@ -265,8 +270,8 @@ def main():
                    "kv": "int8 + fp32 per-token/head scales", "tokens": 30720, "chunk": 512,
                    "parallelism": "single GPU"},
         "prefill": {"attention_kernel_ms_per_layer": round(attn_ms, 4), "combine_ms_per_layer": round(combine_ms, 4),
-                    "append_ms_per_layer": round(ks["batch_rope_int8"][0] / args.steps, 4),
-                    "query_pack_ms_per_layer": round(ks["attention_query_grouped_half"][0] / args.steps, 4),
+                    "append_ms_per_layer": round(ks["batch_rope_int8"][0], 4),
+                    "query_pack_ms_per_layer": round(ks["attention_query_grouped_half"][0], 4),
                     "attention_launches_per_layer": launches,
                     "mfma_fraction_end_to_end": round(flops / (wall_ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4)},
         "roofline": {"bound": "mfma", "kernel": "prefill_int8_kernel (attention_online_int8_q32_k256_r2)",
@@ -278,30 +283,35 @@ def main():
     control = Fp16ControlWorkload(work)
     for _ in range(args.warmup):
         control.step()
-    device.reset_wall_timing(all_kernels=True)
+    device.reset_wall_timing(sample_attention=True)
     t0 = time.perf_counter()
     for _ in range(args.steps):
         control.step()
     fp16_ms = (time.perf_counter() - t0) * 1000.0 / args.steps
-    kc = kernel_stats(device, ["attention_online_q32_k256_s8_g8_r2", "attention_online_fp16.combine", "batch_rope"])
+    kc = kernel_stats(device, ["attention_online_q32_k256_s8_g8_r2", "attention_online_fp16.combine"])
+    device.reset_wall_timing(all_kernels=True)
+    control.step()
+    kc.update(kernel_stats(device, ["batch_rope"]))
     result["fp16_kv_control"] = {
         "ms_per_layer": round(fp16_ms, 4),
         "attention_kernel_ms_per_layer": round(kc["attention_online_q32_k256_s8_g8_r2"][0] / args.steps, 4),
         "combine_ms_per_layer": round(kc.get("attention_online_fp16.combine", (0.0, 0))[0] / args.steps, 4),
-        "append_ms_per_layer": round(kc["batch_rope"][0] / args.steps, 4),
+        "append_ms_per_layer": round(kc["batch_rope"][0], 4),
         "int8_over_fp16_time": round(wall_ms / fp16_ms, 4),
         "kv_bytes_30k": {"int8_with_scales": 30720 * 1040, "fp16": 30720 * 2048}}
     if not args.no_decode:
         dec = DecodeWorkload(device)
         dec.run()  # warm
-        device.reset_wall_timing(all_kernels=True)
+        device.reset_wall_timing(sample_attention=True)
         t0 = time.perf_counter()
         dec.run()
         dec_wall = (time.perf_counter() - t0) * 1000.0 / dec.steps
-        kd = kernel_stats(device, ["attention_decode_int8", "attention_decode_int8.combine", "batch_rope_int8"])
+        kd = kernel_stats(device, ["attention_decode_int8", "attention_decode_int8.combine"])
         dec_kernel_ms = kd["attention_decode_int8"][0] / dec.steps
         dec_comb_ms = kd.get("attention_decode_int8.combine", (0.0, 0))[0] / dec.steps
-        append_ms = kd["batch_rope_int8"][0] / dec.steps
+        device.reset_wall_timing(all_kernels=True)   # append breakdown, not timed
+        dec.run()
+        append_ms = kernel_stats(device, ["batch_rope_int8"])["batch_rope_int8"][0] / dec.steps
         bytes_per_step = dec.kv_bytes() / dec.steps
         dec.bulk_append()
         device.reset_wall_timing(all_kernels=True)

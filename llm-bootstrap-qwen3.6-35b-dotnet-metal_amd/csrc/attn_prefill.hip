@@ -697,29 +697,55 @@ __global__ __launch_bounds__(512, 1) void prefill_pp_kernel(PrefillParams p) {
     }
 }
 
-// One block per (group, tile, logical row); thread d merges the splits.
+// Merges the split partials (O^T scaled by vs_ref, m, l in base 2): one wave per
+// logical row, four dimensions per lane; the maxima of all splits first, then the
+// partials eight splits at a time so their loads are in flight together.
 template <int kTileRows>
 __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillParams p) {
     constexpr size_t kStride = (size_t)kTileRows * 256 + 2 * kTileRows;
-    const uint32_t local_row = blockIdx.x, tile = blockIdx.y, g = blockIdx.z;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t local_row = blockIdx.x * 4 + (threadIdx.x >> 6), tile = blockIdx.y, g = blockIdx.z;
     const uint32_t row = tile * kTileRows + local_row;
-    if (row >= p.rows * 8) return;
+    if (row >= p.rows * 8) return;   // wave-uniform
     const float *base = p.partial + ((size_t)g * p.tiles + tile) * p.splits * kStride;
     float mmax = -INFINITY;
-    for (uint32_t s = 0; s < p.splits; s++) mmax = fmaxf(mmax, base[s * kStride + (size_t)kTileRows * 256 + local_row]);
-    const int d = threadIdx.x;
-    float lsum = 0.0f, osum = 0.0f;
-    for (uint32_t s = 0; s < p.splits; s++) {
-        const float *part = base + s * kStride;
-        const float ms = part[(size_t)kTileRows * 256 + local_row];
-        if (ms == -INFINITY) continue;
-        const float f = __builtin_amdgcn_exp2f(ms - mmax);
-        lsum += part[(size_t)kTileRows * 256 + kTileRows + local_row] * f;
-        osum += part[(size_t)local_row * 256 + d] * f;
+    for (uint32_t s = lane; s < p.splits; s += 64) mmax = fmaxf(mmax, base[s * kStride + (size_t)kTileRows * 256 + local_row]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, o, 64));
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float lsum = 0.0f;
+    for (uint32_t s0 = 0; s0 < p.splits; s0 += 8) {
+        float ms[8], ls[8];
+        float4 os[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t s = min(s0 + j, p.splits - 1);
+            const float *part = base + s * kStride;
+            ms[j] = s0 + j < p.splits ? part[(size_t)kTileRows * 256 + local_row] : -INFINITY;
+            ls[j] = part[(size_t)kTileRows * 256 + kTileRows + local_row];
+            os[j] = *reinterpret_cast<const float4 *>(part + (size_t)local_row * 256 + 4 * lane);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            if (ms[j] == -INFINITY) continue;
+            const float f = __builtin_amdgcn_exp2f(ms[j] - mmax);
+            lsum += ls[j] * f;
+            acc.x += os[j].x * f;
+            acc.y += os[j].y * f;
+            acc.z += os[j].z * f;
+            acc.w += os[j].w * f;
+        }
     }
     const uint32_t token = row / 8, head = g * 8 + row % 8;
-    const size_t at = ((size_t)token * 16 + head) * 256 + d;
-    p.y[at] = osum / lsum * sigmoidf(p.gate[at]);
+    const size_t at = ((size_t)token * 16 + head) * 256 + 4 * lane;
+    const float4 gv = *reinterpret_cast<const float4 *>(p.gate + at);
+    const float inv = 1.0f / lsum;
+    float4 out;
+    out.x = acc.x * inv * sigmoidf(gv.x);
+    out.y = acc.y * inv * sigmoidf(gv.y);
+    out.z = acc.z * inv * sigmoidf(gv.z);
+    out.w = acc.w * inv * sigmoidf(gv.w);
+    *reinterpret_cast<float4 *>(p.y + at) = out;
 }
 
 inline bool aligned(const void *ptr, uintptr_t a) { return (reinterpret_cast<uintptr_t>(ptr) & (a - 1)) == 0; }
@@ -790,9 +816,9 @@ const char *launch_prefill(Context &c, const View *b, int count, const boot_kern
     if (splits > 1) {
         context_split(c, int8 ? "attention_online_int8.combine" : "attention_online_fp16.combine");
         if (int8)
-            prefill_combine_kernel<kPPRows><<<dim3(kPPRows, p.tiles, 2), 256, 0, context_stream(c)>>>(p);
+            prefill_combine_kernel<kPPRows><<<dim3(kPPRows / 4, p.tiles, 2), 256, 0, context_stream(c)>>>(p);
         else
-            prefill_combine_kernel<kRows><<<dim3(kRows, p.tiles, 2), 256, 0, context_stream(c)>>>(p);
+            prefill_combine_kernel<kRows><<<dim3(kRows / 4, p.tiles, 2), 256, 0, context_stream(c)>>>(p);
     }
     return nullptr;
 }

@@ -14,12 +14,14 @@
 // +-127. The library is built without fast-math, with correctly rounded fp32
 // division, so these are the IEEE operations the reference specifies.
 #include "common.h"
+#include "mfma.h"
 
 namespace boot {
 namespace {
 
-constexpr int kTile = 64;               // tokens per store work-group (page-aligned tiles)
-constexpr int kVtStride = 68;           // bytes per LDS row of the V transpose (17 dwords)
+constexpr int kTile = 16;               // tokens per store work-group (page-aligned tiles): 4 per wave
+constexpr int kVtStride = 20;           // bytes per LDS row of the V transpose (5 dwords: byte writes
+                                        // of a wave's 64 rows fall in 64 different banks)
 
 __device__ inline float wave_max(float v) {
 #pragma unroll
@@ -117,7 +119,7 @@ struct KNorm {
     float eps;
 };
 
-// Quantizes and appends tokens [lo, hi) of one 64-token tile for one KV head.
+// Quantizes and appends tokens [lo, hi) of one 16-token tile for one KV head.
 // K: one wave per token, float4 per lane, codes written token-major as char4.
 // V: codes transposed in LDS, then written as page rows (16-byte stores for a
 // full tile, byte stores at partial tile edges), kernels.metal:126-128.
@@ -130,8 +132,9 @@ __device__ void store_tile(const float *__restrict__ k, const float *__restrict_
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t tile0 = tile * kTile;
     const uint32_t lo = max(tile0, pos), hi = min(tile0 + kTile, pos + rows);
-    // Each wave takes tokens wave, wave+4, ...; four tokens' loads are issued
-    // before any is quantized so that several requests are in flight.
+    // Each wave takes tokens wave, wave+4, wave+8, wave+12 of the tile; their four
+    // loads are issued before any is quantized so that the requests are in flight
+    // together.
     for (uint32_t tb = wave; tb < kTile; tb += 16) {
         float4 kx[4];
         float vx[4][4];
@@ -171,12 +174,10 @@ __device__ void store_tile(const float *__restrict__ k, const float *__restrict_
     __syncthreads();
     const uint64_t base = ((uint64_t)(tile0 >> 8) * 2 + h) * kPageBytes + (tile0 & 255);
     if (lo == tile0 && hi == tile0 + kTile) {
-        for (int item = threadIdx.x; item < 256 * 4; item += 256) {
-            const int d = item >> 2, s = item & 3;
-            const uint32_t *src = reinterpret_cast<const uint32_t *>(vt + d * kVtStride + s * 16);
-            *reinterpret_cast<uint4 *>(vc + base + (uint64_t)d * 256 + s * 16) =
-                make_uint4(src[0], src[1], src[2], src[3]);
-        }
+        // thread d writes the tile's 16 bytes of page row d
+        const int d = threadIdx.x;
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(vt + d * kVtStride);
+        *reinterpret_cast<uint4 *>(vc + base + (uint64_t)d * 256) = make_uint4(src[0], src[1], src[2], src[3]);
     } else {
         // partial tile (chunk edges, single-token decode appends): only the valid bytes
         const uint32_t count = hi - lo, first = lo - tile0;
@@ -329,17 +330,20 @@ __global__ __launch_bounds__(256) void batch_split_q_kernel(const float *__restr
 
 __global__ __launch_bounds__(256) void query_grouped_half_kernel(const float *__restrict__ x,
                                                                  _Float16 *__restrict__ y,
-                                                                 uint32_t rows, uint32_t group) {
-    // kernels.metal:1276-1281, four values per thread
-    const uint64_t at = ((uint64_t)blockIdx.x * 256 + threadIdx.x) * 4;
-    if (at >= (uint64_t)rows * 4096) return;
-    const uint64_t d = at % 256, logical = at / 256, span = (uint64_t)rows * group;
-    const uint64_t block = logical / span, local = logical % span;
-    const uint64_t row = local / group, head = block * group + local % group;
-    const float4 v = *reinterpret_cast<const float4 *>(x + (row * 16 + head) * 256 + d);
-    typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-    half4 o = {(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};   // RNE
-    *reinterpret_cast<half4 *>(y + at) = o;
+                                                                 uint32_t rows, uint32_t group_log2) {
+    // kernels.metal:1276-1281: y[(h / A) * M + row][h % A] = half(x[row][h]), eight values per
+    // thread, read in source order; A is a power of two (it divides 16)
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * 512) return;
+    const uint32_t vec = i >> 5, d0 = (i & 31) * 8;              // vec = row * 16 + h
+    const uint32_t row = vec >> 4, h = vec & 15;
+    const uint32_t gmask = (1u << group_log2) - 1;
+    const uint32_t dst = (((h >> group_log2) * rows + row) << group_log2) + (h & gmask);
+    const float4 a = *reinterpret_cast<const float4 *>(x + (size_t)vec * 256 + d0);
+    const float4 b = *reinterpret_cast<const float4 *>(x + (size_t)vec * 256 + d0 + 4);
+    const half8 o = {(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w,
+                     (_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};   // RNE
+    *reinterpret_cast<half8 *>(y + (size_t)dst * 256 + d0) = o;
 }
 
 __global__ __launch_bounds__(256) void fill_zero_kernel(uint4 *__restrict__ p, uint64_t n16,
@@ -412,10 +416,11 @@ const char *launch_query_grouped_half(Context &c, const View *b, int count, cons
     if (rows == 0) return nullptr;
     BOOT_REQUIRE(p.a >= 1 && p.a <= 16 && 16 % p.a == 0, "group size A must divide 16");
     BOOT_REQUIRE(b[0].bytes >= rows * 16384 && b[1].bytes >= rows * 8192, "query buffers smaller than rows*4096 values");
-    BOOT_REQUIRE(aligned(b[0].ptr, 16) && aligned(b[1].ptr, 8), "query bindings misaligned");
-    const uint64_t threads = rows * 1024;
+    BOOT_REQUIRE(rows <= 262144, "rows exceed the 262144-token window");
+    BOOT_REQUIRE(aligned(b[0].ptr, 16) && aligned(b[1].ptr, 16), "query bindings must be 16-byte aligned");
+    const uint64_t threads = rows * 512;
     query_grouped_half_kernel<<<(uint32_t)((threads + 255) / 256), 256, 0, context_stream(c)>>>(
-        (const float *)b[0].ptr, (_Float16 *)b[1].ptr, (uint32_t)rows, p.a);
+        (const float *)b[0].ptr, (_Float16 *)b[1].ptr, (uint32_t)rows, (uint32_t)__builtin_ctz(p.a));
     return nullptr;
 }
 
