@@ -6,13 +6,15 @@
 //     FP32 scores in a caller buffer; serves serial decode and speculative
 //     verification unchanged (QwenEngine.cs:161-165, Prefill.cs:280-285).
 //   * attention_decode_int8: one fused split-K pass that streams the INT8 K/V
-//     pages from HBM once. Scores and PV run on MFMA with FP32-faithful
-//     operands: the FP32 query is split into FP16 hi + lo halves that fill the
-//     16 MFMA columns (8 heads x {hi, lo}), and the scaled probabilities
-//     p*vs[t]/vs_ref (vs_ref = the largest V scale of the split, so they lie in
-//     [0, 1]) likewise into FP16 hi + lo. INT8 codes are dequantized exactly
-//     in registers; scales are applied to scores and probabilities as the
-//     reference does (score = dot * ks[t] / 16, P = p * vs[t]).
+//     pages from HBM once. Scores run on INT8 MFMA straight from the K codes:
+//     the FP32 query of each head is split into two INT8 parts,
+//     q ~= s_q (q1 + q2 / 254) with s_q = max|q| / 127 (error <= 1.55e-5 max|q|),
+//     which fill the 16 MFMA columns (8 heads x {q1, q2}). PV runs on FP16 MFMA
+//     with V codes dequantized exactly in registers and the scaled
+//     probabilities p*vs[t]/vs_ref (vs_ref = the largest V scale of the split, so
+//     they lie in [0, 1]) split into FP16 hi + lo. Scales are applied to scores
+//     and probabilities as the reference does (score = dot * ks[t] / 16,
+//     P = p * vs[t]).
 #include "common.h"
 #include "mfma.h"
 
@@ -117,10 +119,8 @@ __global__ __launch_bounds__(256) void values_int8_kernel(const float *__restric
 // ---------------------------------------------------------------- fused split-K decode
 
 constexpr int kDecodeBlock = 32;                 // tokens per MFMA block
-constexpr int kWaveBlocks = 4;                   // blocks per wave (128 tokens)
-constexpr int kWaveTokens = kDecodeBlock * kWaveBlocks;
 constexpr int kDecodeWaves = 4;
-constexpr int kSplitTokens = kDecodeWaves * kWaveTokens;   // 512 tokens per work-group
+constexpr int kMaxSplitTokens = 2048;            // tokens per work-group at most (LDS scales)
 constexpr int kPartialFloats = 8 * 256 + 16;    // O[8][256], m[8], l[8] per (row, group, split)
 constexpr int kMaxDecodeSplits = 1024;
 constexpr float kLog2e = 1.4426950408889634f;
@@ -135,6 +135,7 @@ struct DecodeParams {
     float *y;
     float *partial;
     uint32_t rows, pos, splits;
+    uint32_t split_blocks;   // 32-token blocks per split
 };
 
 __device__ inline float sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }
@@ -163,97 +164,125 @@ __device__ inline void load_block(DecodeBlock &blk, const DecodeParams &p, uint3
     for (int dt = 0; dt < 16; dt++) blk.v[dt] = *reinterpret_cast<const uint2 *>(vbase + (size_t)dt * 16 * 256);
 }
 
-// Grid: (splits of 512 tokens, 2 KV groups, rows); 4 waves x 4 blocks of 32
-// tokens, two work-groups per CU. Each wave walks its blocks with the loads of
-// the next block in flight while the current one is computed. Per block:
-// S^T[t][n] = K[t] . Qx[n] (16x16x32 FP16 MFMA, n = 8 heads x {hi, lo}; the
-// query operands, identical for the four waves, are read from LDS), the online
-// softmax of the 8 heads in base 2, and O^T[d][n] += V^T[d][t] . Px[t][n]
-// (16x16x32 FP16 MFMA) with Px = p * vs / vs_ref split into FP16 hi + lo; vs_ref,
-// the split's largest V scale, keeps Px in [0, 1] and multiplies the result once.
+// Grid: (splits, 2 KV groups, rows). A split is split_blocks blocks of 32 tokens
+// (chosen on the host so that the grid fits the CUs in one round); wave w takes
+// blocks w, w+4, w+8, ... so the four waves consume each 128-byte V page-row
+// line (128 tokens) together and lines are fetched once. Each wave walks its
+// blocks with the loads of the next block in flight while the current one is
+// computed. Per block: S^T[t][n] = K[t] . Qx[n] (16x16x64 INT8 MFMA on the raw K
+// codes, n = 8 heads x {q1, q2}), the online softmax of the 8 heads in base 2,
+// and O^T[d][n] += V^T[d][t] . Px[t][n] (16x16x32 FP16 MFMA) with
+// Px = p * vs / vs_ref split into FP16 hi + lo; vs_ref, the split's largest V
+// scale, keeps Px in [0, 1] and multiplies the result once.
 // Lane l holds MFMA column n = l % 16 and token/k group qq = l / 16.
 __global__ __launch_bounds__(256, 2) void decode_int8_kernel(DecodeParams p) {
+    typedef int v4i __attribute__((ext_vector_type(4)));
     __shared__ float merge_o[kDecodeWaves][8][256];
     __shared__ float merge_m[kDecodeWaves][8], merge_l[kDecodeWaves][8];
-    __shared__ float kscale[kSplitTokens], vscale[kSplitTokens];
-    __shared__ __attribute__((aligned(16))) _Float16 qlds[8][64][8];   // [MFMA c][lane][8 dims]
-    __shared__ float red[kDecodeWaves];
+    __shared__ float kscale[kMaxSplitTokens], vscale[kMaxSplitTokens];
+    __shared__ float red[kDecodeWaves], qmax[kDecodeWaves][8];
+    __shared__ v4i qlds[4][64];    // INT8 query operands, [MFMA c][lane]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, qq = lane >> 4, head = n & 7;
     const bool lo_col = n >= 8;
     const uint32_t split = blockIdx.x, g = blockIdx.y, row = blockIdx.z;
     const uint32_t length = p.pos + row + 1;
-    const uint32_t begin = split * kSplitTokens;
-    const uint32_t end = min(length, begin + kSplitTokens);
-    // Wave w takes blocks w, w+4, w+8, w+12 of the split: the four waves consume each
-    // 128-byte V page-row line (128 tokens) together, so lines are fetched once.
-    const uint32_t first = begin + wave * kDecodeBlock;
+    const uint32_t split_tokens = p.split_blocks * kDecodeBlock;
+    const uint32_t begin = split * split_tokens;
+    const uint32_t end = min(length, begin + split_tokens);
+    const uint32_t nblocks = end > begin ? (end - begin + kDecodeBlock - 1) / kDecodeBlock : 0;
 
+    // ---- the small loads first (scales of the split, this wave's query chunk), then
+    // the first K/V block: waits on the memory counter are in order, so the set-up
+    // below never waits for the block
+    // (a fixed count of loads, no branches: the counter waits below stay exact;
+    // indices past the split repeat its last token, a cache hit)
+    const uint32_t last = (end > begin ? end : length) - 1;
+    float ksv[kMaxSplitTokens / 256], vsv[kMaxSplitTokens / 256];
+#pragma unroll
+    for (int it = 0; it < kMaxSplitTokens / 256; it++) {
+        const size_t at = (size_t)min(begin + tid + 256 * it, last) * 2 + g;
+        ksv[it] = p.ks[at];
+        vsv[it] = p.vs[at];
+    }
+    // query chunk c = wave: lane (n, qq) takes dims 64c + 16qq + [0, 16) of head n % 8
+    float4 x[4];
+    {
+        const float *qh = p.q + ((size_t)row * 16 + g * 8 + head) * 256 + 64 * wave + 16 * qq;
+#pragma unroll
+        for (int f = 0; f < 4; f++) x[f] = *reinterpret_cast<const float4 *>(qh + 4 * f);
+    }
+    // unconditional (a wave without blocks re-reads the first one, a cache hit): the
+    // counter waits stay exact
     DecodeBlock cur, nxt;
-    if (first < end) load_block(cur, p, g, first, length, lane, n, qq);
+    load_block(cur, p, g, begin + ((uint32_t)wave < nblocks ? wave : 0) * kDecodeBlock, length, lane, n, qq);
 
-    // ---- scales of the split (this group) into LDS, vs_ref = their maximum
+    // ---- scales of the split (this group) into LDS, vs_ref = their maximum; the
+    // per-head maxima of the query chunks
     float vmax = 0.0f;
-    for (int e = tid; e < kSplitTokens; e += 256) {
-        const uint32_t t = begin + e;
-        const bool inside = t < end;
-        const float ksv = inside ? p.ks[(size_t)t * 2 + g] : 0.0f;
-        const float vsv = inside ? p.vs[(size_t)t * 2 + g] : 0.0f;
-        kscale[e] = ksv * (kLog2e / 16.0f);
-        vscale[e] = vsv;
-        vmax = fmaxf(vmax, vsv);
+#pragma unroll
+    for (int it = 0; it < kMaxSplitTokens / 256; it++) {
+        const uint32_t e = tid + 256 * it;   // < kMaxSplitTokens; entries past the split are never read
+        // masked by a multiply, not a select: every load above stays unconditional
+        // (the clamped indices never reach a poisoned, non-finite tail scale)
+        const float inside = begin + e < end ? 1.0f : 0.0f;
+        kscale[e] = ksv[it] * (kLog2e / 16.0f) * inside;
+        vscale[e] = vsv[it] * inside;
+        vmax = fmaxf(vmax, vsv[it] * inside);
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) vmax = fmaxf(vmax, __shfl_xor(vmax, o, 64));
     if (lane == 0) red[wave] = vmax;
-    // ---- query operands, built once per work-group: MFMA c covers dims
-    // d(c, qq, e) = 64*(c/2) + 16*qq + 8*(c%2) + e, matching the 16-byte K loads
-    {
-        const int c = wave * 2;   // each wave builds two of the eight operands
-        const float *qh = p.q + ((size_t)row * 16 + g * 8 + head) * 256;
+    float amax = 0.0f;
 #pragma unroll
-        for (int cc = 0; cc < 2; cc++) {
-            const float *src = qh + 64 * ((c + cc) >> 1) + 16 * qq + 8 * ((c + cc) & 1);
-            const float4 x0 = *reinterpret_cast<const float4 *>(src);
-            const float4 x1 = *reinterpret_cast<const float4 *>(src + 4);
-            const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-            half8 op;
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const _Float16 hi = (_Float16)x[e];
-                op[e] = lo_col ? (_Float16)(x[e] - (float)hi) : hi;
-            }
-            *reinterpret_cast<half8 *>(&qlds[c + cc][lane][0]) = op;
-        }
-    }
+    for (int f = 0; f < 4; f++) amax = fmaxf(amax, fmaxf(fmaxf(fabsf(x[f].x), fabsf(x[f].y)), fmaxf(fabsf(x[f].z), fabsf(x[f].w))));
+    amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    if (lane < 8) qmax[wave][lane] = amax;
     __syncthreads();
     const float vs_ref = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     const float vs_inv = vs_ref > 0.0f ? 1.0f / vs_ref : 0.0f;
+    // ---- INT8 query operand of chunk c = wave: part n / 8 of q ~= s_q (q1 + q2 / 254)
+    const float qabs = fmaxf(fmaxf(qmax[0][head], qmax[1][head]), fmaxf(qmax[2][head], qmax[3][head]));
+    const float qsc = qabs * (1.0f / 127.0f);   // s_q of the lane's head
+    {
+        const float inv = qabs > 0.0f ? 127.0f / qabs : 0.0f;
+        auto part = [&](float v) {
+            const float z = v * inv, q1 = rintf(z);
+            const float q = lo_col ? rintf((z - q1) * 254.0f) : q1;
+            return (uint32_t)(uint8_t)(int8_t)(int)fminf(fmaxf(q, -127.0f), 127.0f);
+        };
+        uint32_t w[4];
+#pragma unroll
+        for (int f = 0; f < 4; f++) w[f] = part(x[f].x) | (part(x[f].y) << 8) | (part(x[f].z) << 16) | (part(x[f].w) << 24);
+        qlds[wave][lane] = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+    }
+    __syncthreads();
+    v4i qi[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) qi[c] = qlds[c][lane];
 
     floatx4 o[16];
 #pragma unroll
     for (int i = 0; i < 16; i++) o[i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     float m = -INFINITY, l = 0.0f;
 
-    for (int b = 0; b < kWaveBlocks; b++) {
-        const uint32_t t0 = first + b * kDecodeWaves * kDecodeBlock;
-        if (t0 >= end) break;                                   // wave-uniform
-        const bool more = b + 1 < kWaveBlocks && t0 + kDecodeWaves * kDecodeBlock < end;
-        if (more) load_block(nxt, p, g, t0 + kDecodeWaves * kDecodeBlock, length, lane, n, qq);
-        floatx4 s[2];
+    for (uint32_t b = wave; b < nblocks; b += kDecodeWaves) {
+        const uint32_t t0 = begin + b * kDecodeBlock;
+        const bool more = b + kDecodeWaves < nblocks;            // wave-uniform
+        // the last block re-reads itself (a cache hit) rather than branching
+        load_block(nxt, p, g, more ? t0 + kDecodeWaves * kDecodeBlock : t0, length, lane, n, qq);
+        v4i s[2];
 #pragma unroll
         for (int a = 0; a < 2; a++) {
-            floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+            v4i acc = {0, 0, 0, 0};
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const half8 q0 = *reinterpret_cast<const half8 *>(&qlds[2 * j][lane][0]);
-                const half8 q1 = *reinterpret_cast<const half8 *>(&qlds[2 * j + 1][lane][0]);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_half8(cur.k[a][j].x, cur.k[a][j].y), q0, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_half8(cur.k[a][j].z, cur.k[a][j].w), q1, acc, 0, 0, 0);
-            }
+            for (int j = 0; j < 4; j++)
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, cur.k[a][j]), qi[j], acc, 0, 0, 0);
             s[a] = acc;
         }
-        // C layout: lane (n, qq) holds rows 4*qq + r -> token t0 + 8*qq + 4*a + r.
+        // C layout: lane (n, qq) holds rows 4*qq + r -> token t0 + 8*qq + 4*a + r; the
+        // partner column n ^ 8 holds the other part of the same head.
         const int local0 = (int)(t0 - begin) + 8 * qq;          // token offset inside the split
         float sc[8];
         float top = -INFINITY;
@@ -261,7 +290,8 @@ __global__ __launch_bounds__(256, 2) void decode_int8_kernel(DecodeParams p) {
         for (int a = 0; a < 2; a++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const float full = s[a][r] + __shfl_xor(s[a][r], 8, 64);   // hi + lo columns
+                const int mine = s[a][r], other = __shfl_xor(mine, 8, 64);
+                const float full = ((float)(lo_col ? other : mine) + (float)(lo_col ? mine : other) * (1.0f / 254.0f)) * qsc;
                 const uint32_t t = t0 + 8 * qq + 4 * a + r;
                 const float value = t < end ? full * kscale[local0 + 4 * a + r] : -INFINITY;
                 sc[a * 4 + r] = value;
@@ -299,7 +329,9 @@ __global__ __launch_bounds__(256, 2) void decode_int8_kernel(DecodeParams p) {
 #pragma unroll
         for (int dt = 0; dt < 16; dt++)
             o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_half8(cur.v[dt].x, cur.v[dt].y), pop, o[dt], 0, 0, 0);
-        if (more) cur = nxt;
+        // the copy waits for the prefetched block: keep it after this block's MFMAs
+        __builtin_amdgcn_sched_barrier(0);
+        cur = nxt;
     }
 
     // ---- merge the four waves: O^T[d][n] with d = 16*dt + 4*qq + r; heads sum hi + lo columns;
@@ -307,8 +339,7 @@ __global__ __launch_bounds__(256, 2) void decode_int8_kernel(DecodeParams p) {
     if (n < 8) {
 #pragma unroll
         for (int dt = 0; dt < 16; dt++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) merge_o[wave][head][16 * dt + 4 * qq + r] = o[dt][r];
+            *reinterpret_cast<floatx4 *>(&merge_o[wave][head][16 * dt + 4 * qq]) = o[dt];
         if (qq == 0) {
             merge_m[wave][head] = m;
             merge_l[wave][head] = l;
@@ -317,9 +348,7 @@ __global__ __launch_bounds__(256, 2) void decode_int8_kernel(DecodeParams p) {
     __syncthreads();
     if (n >= 8) {
 #pragma unroll
-        for (int dt = 0; dt < 16; dt++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) merge_o[wave][head][16 * dt + 4 * qq + r] += o[dt][r];
+        for (int dt = 0; dt < 16; dt++) *reinterpret_cast<floatx4 *>(&merge_o[wave][head][16 * dt + 4 * qq]) += o[dt];
     }
     __syncthreads();
     // thread -> (head h, 8 dims); combine waves with their maxima
@@ -343,64 +372,104 @@ __global__ __launch_bounds__(256, 2) void decode_int8_kernel(DecodeParams p) {
         return;
     }
     float *part = p.partial + (((size_t)row * 2 + g) * p.splits + split) * kPartialFloats;
-    for (int e = 0; e < 8; e++) part[h * 256 + d0 + e] = acc[e];
+    *reinterpret_cast<float4 *>(part + h * 256 + d0) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    *reinterpret_cast<float4 *>(part + h * 256 + d0 + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
     if ((threadIdx.x & 31) == 0) {
         part[2048 + h] = mw;
         part[2056 + h] = lw;
     }
 }
 
-// Merges the splits of one (row, head) slice of 16 dims. 256 threads = 16
-// split groups x 16 dims: every thread streams every 16th split with
-// independent loads, the split weights exp2(m_s - max) are computed once into
-// LDS, and the 16 group sums are added in LDS.
+// Merges the splits of one (row, head) for 64 dimensions (grid: 4 dimension
+// chunks x 16 heads x rows). Two memory round trips: thread s first loads m_s
+// and l_s of every split at once (the block maximum, the weights
+// exp2(m_s - max) into LDS and the weighted sum of l), then 4 groups of 64 lanes
+// stream the float4 partials of every 4th split and the groups are added in LDS.
 __global__ __launch_bounds__(256) void decode_combine_kernel(const float *__restrict__ partial, const float *__restrict__ gate,
                                                              float *__restrict__ y, uint32_t splits) {
     __shared__ float weight[kMaxDecodeSplits];
-    __shared__ float red[4];
-    __shared__ float sums[16][17];
+    __shared__ float red[4], lred[4];
+    __shared__ float4 sums[4][16];
     const uint32_t row = blockIdx.z, hq = blockIdx.y, g = hq / 8, h = hq % 8;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float *base = partial + ((size_t)row * 2 + g) * splits * kPartialFloats;
+    constexpr int kPer = kMaxDecodeSplits / 256;
+    float ms[kPer], ls[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; i++) {
+        const uint32_t sidx = min((uint32_t)(tid + 256 * i), splits - 1);
+        ms[i] = tid + 256 * i < (int)splits ? base[(size_t)sidx * kPartialFloats + 2048 + h] : -INFINITY;
+        ls[i] = base[(size_t)sidx * kPartialFloats + 2056 + h];
+    }
     float mmax = -INFINITY;
-    for (uint32_t s = tid; s < splits; s += 256) mmax = fmaxf(mmax, base[(size_t)s * kPartialFloats + 2048 + h]);
+#pragma unroll
+    for (int i = 0; i < kPer; i++) mmax = fmaxf(mmax, ms[i]);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, o, 64));
     if (lane == 0) red[wave] = mmax;
     __syncthreads();
     mmax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     float lsum = 0.0f;
-    for (uint32_t s = tid; s < splits; s += 256) {
-        const float *part = base + (size_t)s * kPartialFloats;
-        const float ms = part[2048 + h];
-        const float w = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - mmax);
-        weight[s] = w;
-        lsum += part[2056 + h] * w;
+#pragma unroll
+    for (int i = 0; i < kPer; i++) {
+        if (tid + 256 * i >= (int)splits) continue;
+        const float w = ms[i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms[i] - mmax);
+        weight[tid + 256 * i] = w;
+        lsum += ls[i] * w;
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o, 64);
+    if (lane == 0) lred[wave] = lsum;
     __syncthreads();
-    if (lane == 0) red[wave] = lsum;
-    __syncthreads();
-    lsum = (red[0] + red[1]) + (red[2] + red[3]);
-    const int grp = tid >> 4, dl = tid & 15;
-    const uint32_t d = blockIdx.x * 16 + dl;
+    lsum = (lred[0] + lred[1]) + (lred[2] + lred[3]);
+    // group `wave` takes splits wave, wave + 4, ...; lane: 4 dims of the 64-dim chunk
+    const uint32_t d = blockIdx.x * 64 + 4 * (lane & 15);
+    const int sub = lane >> 4;   // 4 sub-lanes per dim quad: splits wave + 4 (4j + sub)
     const float *col = base + (size_t)h * 256 + d;
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    uint32_t s = grp;
-    for (; s + 48 < splits; s += 64) {
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (uint32_t s0 = wave + 4 * sub; s0 < splits; s0 += 64) {
+        float4 v[4];
+        float w[4];
 #pragma unroll
-        for (int u = 0; u < 4; u++) acc[u] += col[(size_t)(s + 16 * u) * kPartialFloats] * weight[s + 16 * u];
+        for (int u = 0; u < 4; u++) {
+            const uint32_t sidx = s0 + 16 * u;
+            const bool in = sidx < splits;
+            v[u] = *reinterpret_cast<const float4 *>(col + (size_t)min(sidx, splits - 1) * kPartialFloats);
+            w[u] = in ? weight[sidx] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            acc.x += v[u].x * w[u];
+            acc.y += v[u].y * w[u];
+            acc.z += v[u].z * w[u];
+            acc.w += v[u].w * w[u];
+        }
     }
-    for (; s < splits; s += 16) acc[0] += col[(size_t)s * kPartialFloats] * weight[s];
-    sums[grp][dl] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    // the 16 (wave, sub) partial sums of each dim quad
+#pragma unroll
+    for (int o = 16; o < 64; o <<= 1) {
+        acc.x += __shfl_xor(acc.x, o, 64);
+        acc.y += __shfl_xor(acc.y, o, 64);
+        acc.z += __shfl_xor(acc.z, o, 64);
+        acc.w += __shfl_xor(acc.w, o, 64);
+    }
+    if (sub == 0) sums[wave][lane] = acc;
     __syncthreads();
     if (tid < 16) {
-        float total = 0.0f;
+        float4 t = sums[0][tid];
 #pragma unroll
-        for (int k = 0; k < 16; k++) total += sums[k][tid];
-        const size_t at = ((size_t)row * 16 + hq) * 256 + blockIdx.x * 16 + tid;
-        y[at] = total / lsum * sigmoidf(gate[at]);
+        for (int w = 1; w < 4; w++) {
+            t.x += sums[w][tid].x;
+            t.y += sums[w][tid].y;
+            t.z += sums[w][tid].z;
+            t.w += sums[w][tid].w;
+        }
+        const size_t at = ((size_t)row * 16 + hq) * 256 + blockIdx.x * 64 + 4 * tid;
+        const float inv = 1.0f / lsum;
+        y[at + 0] = t.x * inv * sigmoidf(gate[at + 0]);   // y and gate need only 4-byte alignment
+        y[at + 1] = t.y * inv * sigmoidf(gate[at + 1]);
+        y[at + 2] = t.z * inv * sigmoidf(gate[at + 2]);
+        y[at + 3] = t.w * inv * sigmoidf(gate[at + 3]);
     }
 }
 
@@ -476,8 +545,15 @@ const char *launch_decode_int8(Context &c, const View *b, int count, const boot_
     BOOT_REQUIRE(aligned(b[0].ptr, 16) && aligned(b[1].ptr, 16) && aligned(b[2].ptr, 16) && aligned(b[3].ptr, 4) &&
                      aligned(b[4].ptr, 4) && aligned(b[5].ptr, 4) && aligned(b[6].ptr, 4),
                  "bindings misaligned (q, k, v need 16 bytes)");
-    // Work-groups of 512 tokens (4 waves x 128); rows and groups in the grid.
-    const uint64_t splits = (length + kSplitTokens - 1) / kSplitTokens;
+    // Split length in 32-token blocks, chosen so that the grid (splits x 2 groups x
+    // rows, two work-groups per CU) fits the CUs in one round: a second, nearly empty
+    // round would double the time. At most kMaxSplitTokens per split.
+    const uint64_t total_blocks = (length + kDecodeBlock - 1) / kDecodeBlock;
+    const uint64_t slots = std::max<uint64_t>(1, 2ull * (uint64_t)std::max(1, context_cus(c)) / (2 * rows));
+    uint64_t split_blocks = (total_blocks + slots - 1) / slots;
+    split_blocks = std::max<uint64_t>(split_blocks, (uint64_t)kDecodeWaves);             // one block per wave at least
+    split_blocks = std::min<uint64_t>(split_blocks, (uint64_t)(kMaxSplitTokens / kDecodeBlock));
+    const uint64_t splits = (total_blocks + split_blocks - 1) / split_blocks;
     BOOT_REQUIRE(splits <= kMaxDecodeSplits, "too many decode splits");
     DecodeParams d;
     d.q = (const float *)b[0].ptr;
@@ -490,6 +566,7 @@ const char *launch_decode_int8(Context &c, const View *b, int count, const boot_
     d.rows = (uint32_t)rows;
     d.pos = p.pos;
     d.splits = (uint32_t)splits;
+    d.split_blocks = (uint32_t)split_blocks;
     d.partial = nullptr;
     if (splits > 1) {
         d.partial = (float *)context_workspace(c, rows * 2 * splits * kPartialFloats * sizeof(float));
@@ -498,7 +575,7 @@ const char *launch_decode_int8(Context &c, const View *b, int count, const boot_
     decode_int8_kernel<<<dim3((uint32_t)splits, 2, (uint32_t)rows), 256, 0, context_stream(c)>>>(d);
     if (splits > 1) {
         context_split(c, "attention_decode_int8.combine");
-        decode_combine_kernel<<<dim3(16, 16, (uint32_t)rows), 256, 0, context_stream(c)>>>(d.partial, d.gate, d.y,
+        decode_combine_kernel<<<dim3(4, 16, (uint32_t)rows), 256, 0, context_stream(c)>>>(d.partial, d.gate, d.y,
                                                                                         (uint32_t)splits);
     }
     return nullptr;
