@@ -344,12 +344,16 @@ constexpr int kPPVStride = kPPKeys + 8;    // FP16 V^T tile row stride (halves):
 constexpr size_t kPPPartialStride = (size_t)kPPRows * 256 + 2 * kPPRows;
 constexpr int kPPQRegs = 6;                // Q^T operand chunks held in registers; the rest in LDS
 
-// Max and sum over the lane pair (l, l ^ 32): v_permlane32_swap leaves lanes
-// 0-31 of one result and 32-63 of the other holding the pair's two values.
+// Max over the lane pair (l, l ^ 32). v_permlane32_swap exchanges lanes 32-63 of
+// its first operand with lanes 0-31 of its second, so with both holding x every
+// lane ends with its own value in one register and its partner's in the other.
+// Inline assembly: with the builtin, the compiler keeps only the first result when
+// both operands are the same value, and the maximum then misses the partner lane.
+// The no-ops cover the wait states around the cross-lane move.
 __device__ inline float pair_max(float x) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
-                                                    false, false);
-    return fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
+    float a = x, b = x;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+    return fmaxf(a, b);
 }
 
 // v_max3_f32 without the canonicalizing moves the compiler adds in front of

@@ -68,6 +68,51 @@ def test_prefill_matches_fp64(device, oracle, history, rows):
     cache.dispose()
 
 
+@pytest.mark.parametrize("slope", [0.05, 0.6])
+def test_prefill_rising_scores(device, oracle, slope):
+    """Scores that rise along the keys by about `slope` (natural log) per token: the online
+    softmax meets a new maximum tile after tile, so its running maximum is rebased and the
+    accumulator rescaled many times within one split (every 15 / (slope log2 e) tokens)."""
+    history, rows = 3584, 512
+    length = history + rows
+    q = (np.abs(oracle.fill_hash(rows * 4096, 17, 3)) + np.float32(0.25)).astype(np.float32)
+    k, v = reference_kv(length)
+    per_token = slope * 16.0 / float(q.reshape(-1, 256).sum(1).mean())
+    k = np.ascontiguousarray(k / 3 + (per_token * np.arange(length, dtype=np.float32))[:, None, None])
+    kc, vc, ks, vs = oracle.empty_cache(length + 1)
+    oracle.store(k, v, 0, kc, vc, ks, vs)
+    poison_tail(oracle, kc, vc, ks, vs, length)
+    gate = oracle.fill_hash(rows * 4096, 11, 1)
+    cache = upload_cache(device, kc, vc, ks, vs)
+    y = run_prefill(device, q, gate, cache, rows, history)[:-1]
+    assert np.all(np.isfinite(y))
+    ref = oracle.attention(q, kc, vc, ks, vs, gate, rows, history, round_q_half=1)
+    assert rel_l2(y, ref) <= REL_L2 and np.abs(y - ref).max() <= MAX_ABS, (rel_l2(y, ref), np.abs(y - ref).max())
+    cache.dispose()
+
+
+def test_prefill_score_spikes(device, oracle):
+    """Single keys whose scores jump far (tens of log2 units) above all earlier keys, at
+    tile offsets that fall on both halves of the key tile; each spike outgrows the last."""
+    history, rows = 3584, 64
+    length = history + rows
+    q = (np.abs(oracle.fill_hash(rows * 4096, 17, 3)) + np.float32(0.25)).astype(np.float32)
+    k, v = reference_kv(length)
+    k = k / 3
+    for j, token in enumerate((45, 77, 1000, 2059, 3000, 3600, 3620, 3631)):
+        k[token] += np.float32(1.0 + 0.5 * j)
+    kc, vc, ks, vs = oracle.empty_cache(length + 1)
+    oracle.store(np.ascontiguousarray(k), v, 0, kc, vc, ks, vs)
+    poison_tail(oracle, kc, vc, ks, vs, length)
+    gate = oracle.fill_hash(rows * 4096, 11, 1)
+    cache = upload_cache(device, kc, vc, ks, vs)
+    y = run_prefill(device, q, gate, cache, rows, history)[:-1]
+    assert np.all(np.isfinite(y))
+    ref = oracle.attention(q, kc, vc, ks, vs, gate, rows, history, round_q_half=1)
+    assert rel_l2(y, ref) <= REL_L2 and np.abs(y - ref).max() <= MAX_ABS, (rel_l2(y, ref), np.abs(y - ref).max())
+    cache.dispose()
+
+
 def test_prefill_kernel_aliases_agree(device, oracle):
     """The r2, r1 and K128 names of the reference are serviced by the same gfx950 kernel."""
     q, gate, host = build_case(oracle, 257, 33)
