@@ -6,7 +6,8 @@
 //     FP32 scores in a caller buffer; serves serial decode and speculative
 //     verification unchanged (QwenEngine.cs:161-165, Prefill.cs:280-285).
 //   * attention_decode_int8: one fused split-K pass that streams the INT8 K/V
-//     pages from HBM once. Scores run on INT8 MFMA straight from the K codes:
+//     pages from HBM once, as whole K rows and whole 128-byte V page-row lines
+//     staged through LDS. Scores run on INT8 MFMA straight from the K codes:
 //     the FP32 query of each head is split into two INT8 parts,
 //     q ~= s_q (q1 + q2 / 254) with s_q = max|q| / 127 (error <= 1.55e-5 max|q|),
 //     which fill the 16 MFMA columns (8 heads x {q1, q2}). PV runs on FP16 MFMA
@@ -118,11 +119,12 @@ __global__ __launch_bounds__(256) void values_int8_kernel(const float *__restric
 
 // ---------------------------------------------------------------- fused split-K decode
 
-constexpr int kDecodeBlock = 32;                 // tokens per MFMA block
-constexpr int kDecodeWaves = 4;
+constexpr int kChunk = 128;                      // tokens per LDS chunk (one 128-byte line per V page row)
+constexpr int kDecodeWaves = 8;
 constexpr int kMaxSplitTokens = 2048;            // tokens per work-group at most (LDS scales)
 constexpr int kPartialFloats = 8 * 256 + 16;    // O[8][256], m[8], l[8] per (row, group, split)
 constexpr int kMaxDecodeSplits = 1024;
+constexpr int kMergeStride = 256 + 16;            // merge row (floats): the 8 heads of a write spread over the banks
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct DecodeParams {
@@ -135,94 +137,141 @@ struct DecodeParams {
     float *y;
     float *partial;
     uint32_t rows, pos, splits;
-    uint32_t split_blocks;   // 32-token blocks per split
+    uint32_t split_chunks;   // 128-token chunks per split
 };
 
 __device__ inline float sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-struct DecodeBlock {
-    uint4 k[2][4];    // K tiles a = 0, 1: 16 codes at dims 16*qq + 64*j of this lane's token
-    uint2 v[16];      // V^T rows d = 16*dt + n: 8 codes of tokens t0 + 8*qq + [0, 8)
+// One chunk of one KV group in flight: thread t holds K rows t / 16 + 32 i (16 bytes
+// at 16 (t % 16)) and V page-row segments t / 8 + 64 i (16 bytes at 16 (t % 8)),
+// i < 4: every load instruction reads whole 256-byte K rows or whole 128-byte V
+// lines, the pattern that streams at full HBM rate (loads shaped like the MFMA
+// operands, 16 rows per instruction, reach about two thirds of it).
+struct ChunkRegs {
+    uint4 k0, k1, k2, k3, v0, v1, v2, v3;   // named, not an array: kept in registers
 };
 
-// K tile a row i holds token t0 + 8*(i/4) + 4*a + i%4, so after the QK MFMA lane
-// group qq owns tokens t0 + 8*qq + [0, 8), the k-group of the PV MFMA. Addresses
-// are clamped inside the cache; tokens at or beyond the split end are masked.
-__device__ inline void load_block(DecodeBlock &blk, const DecodeParams &p, uint32_t g, uint32_t t0, uint32_t length,
-                                  int lane, int n, int qq) {
-#pragma unroll
-    for (int a = 0; a < 2; a++) {
-        const uint32_t i = lane & 15;
-        const uint32_t t = min(t0 + 8 * (i >> 2) + 4 * a + (i & 3), length - 1);
-        const int8_t *kr = p.k + ((size_t)t * 2 + g) * 256 + 16 * qq;
-#pragma unroll
-        for (int j = 0; j < 4; j++) blk.k[a][j] = *reinterpret_cast<const uint4 *>(kr + 64 * j);
-    }
-    const uint32_t tv = min(t0 + 8 * qq, length - 1) & ~7u;
-    const int8_t *vbase = p.v + value_index((uint64_t)tv * 2 + g, 0) + (size_t)n * 256;
-#pragma unroll
-    for (int dt = 0; dt < 16; dt++) blk.v[dt] = *reinterpret_cast<const uint2 *>(vbase + (size_t)dt * 16 * 256);
+// The LDS image of a chunk. K: 128 token rows of 256 bytes, 16-byte piece c of
+// token t at position c ^ (t % 16). V^T: 256 dimension rows of 128 bytes (the
+// chunk's tokens), piece c (tokens 16c..16c+15) of row d at position c ^ ((d / 2) % 8).
+// Both make the operand reads and the chunk writes free of bank conflicts.
+struct ChunkLds {
+    uint4 k[kChunk][16];
+    uint4 v[256][8];
+};
+
+__device__ __attribute__((always_inline)) inline uint4 load_k_piece(const DecodeParams &p, uint32_t g, uint32_t c0,
+                                                                    uint32_t length, int tid, int i) {
+    const uint32_t t = min(c0 + (uint32_t)(tid >> 4) + 32 * i, length - 1);
+    return *reinterpret_cast<const uint4 *>(p.k + ((size_t)t * 2 + g) * 256 + 16 * (tid & 15));
 }
 
-// Grid: (splits, 2 KV groups, rows). A split is split_blocks blocks of 32 tokens
-// (chosen on the host so that the grid fits the CUs in one round); wave w takes
-// blocks w, w+4, w+8, ... so the four waves consume each 128-byte V page-row
-// line (128 tokens) together and lines are fetched once. Each wave walks its
-// blocks with the loads of the next block in flight while the current one is
-// computed. Per block: S^T[t][n] = K[t] . Qx[n] (16x16x64 INT8 MFMA on the raw K
-// codes, n = 8 heads x {q1, q2}), the online softmax of the 8 heads in base 2,
-// and O^T[d][n] += V^T[d][t] . Px[t][n] (16x16x32 FP16 MFMA) with
-// Px = p * vs / vs_ref split into FP16 hi + lo; vs_ref, the split's largest V
-// scale, keeps Px in [0, 1] and multiplies the result once.
-// Lane l holds MFMA column n = l % 16 and token/k group qq = l / 16.
-__global__ __launch_bounds__(256, 2) void decode_int8_kernel(DecodeParams p) {
+// Chunk idx of the split starting at token `begin`. Past the last chunk the loads
+// stay (a fixed count keeps the counter waits exact) but every lane reads the same
+// 16 bytes of the first one: a cache line instead of a 64 KB re-read that the
+// epilogue would wait for.
+__device__ __attribute__((always_inline)) inline void load_chunk(ChunkRegs &r, const DecodeParams &p, uint32_t g,
+                                                                 uint32_t begin, uint32_t idx, uint32_t nchunks,
+                                                                 uint32_t length, int tid) {
+    const bool real = idx < nchunks;
+    const uint32_t c0 = real ? begin + idx * kChunk : begin;
+    const int lt = real ? tid : 0;
+    r.k0 = load_k_piece(p, g, c0, length, lt, 0);
+    r.k1 = load_k_piece(p, g, c0, length, lt, real ? 1 : 0);
+    r.k2 = load_k_piece(p, g, c0, length, lt, real ? 2 : 0);
+    r.k3 = load_k_piece(p, g, c0, length, lt, real ? 3 : 0);
+    // c0 is a multiple of 128 inside the cache's whole pages
+    const int8_t *vrow = p.v + value_index((uint64_t)c0 * 2 + g, 0) + (size_t)(lt >> 3) * 256 + 16 * (lt & 7);
+    const size_t step = real ? 64 * 256 : 0;
+    r.v0 = *reinterpret_cast<const uint4 *>(vrow);
+    r.v1 = *reinterpret_cast<const uint4 *>(vrow + step);
+    r.v2 = *reinterpret_cast<const uint4 *>(vrow + 2 * step);
+    r.v3 = *reinterpret_cast<const uint4 *>(vrow + 3 * step);
+}
+
+__device__ __attribute__((always_inline)) inline void store_chunk(ChunkLds &b, const ChunkRegs &r, int tid) {
+    const int t = tid >> 4, c = tid & 15;   // K rows t + 32i (t + 32i has the same t % 16)
+    const int kp = c ^ (t & 15);
+    b.k[t][kp] = r.k0;
+    b.k[t + 32][kp] = r.k1;
+    b.k[t + 64][kp] = r.k2;
+    b.k[t + 96][kp] = r.k3;
+    const int d = tid >> 3, e = tid & 7;    // V rows d + 64i (same (d / 2) % 8)
+    const int vp = e ^ ((d >> 1) & 7);
+    b.v[d][vp] = r.v0;
+    b.v[d + 64][vp] = r.v1;
+    b.v[d + 128][vp] = r.v2;
+    b.v[d + 192][vp] = r.v3;
+}
+
+// Grid: (splits, 2 KV groups, rows), one 8-wave work-group per CU; a split is
+// split_chunks chunks of 128 tokens, chosen on the host so that the grid fits the
+// CUs in one round. The work-group streams its chunks through double-buffered LDS
+// with two chunks in flight in registers; per chunk wave w takes tokens 16w..16w+15:
+// S^T[t][n] = K[t] . Qx[n] (16x16x64 INT8 MFMA on the raw K codes, n = 8 heads x
+// {q1, q2}), the online softmax of the 8 heads in base 2, and
+// O^T[d][n] += V^T[d][t] . Px[t][n] (16x16x16 FP16 MFMA) with Px = p * vs / vs_ref
+// split into FP16 hi + lo; vs_ref, the split's largest V scale, keeps Px in [0, 1]
+// and multiplies the result once. Lane l holds MFMA column n = l % 16 and
+// token/k group qq = l / 16.
+__global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
     typedef int v4i __attribute__((ext_vector_type(4)));
-    __shared__ float merge_o[kDecodeWaves][8][256];
+    typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+    // the chunk buffers; after the last chunk the same bytes hold the wave merge
+    __shared__ __attribute__((aligned(16))) unsigned char arena[2 * sizeof(ChunkLds)];
+    static_assert(sizeof(float) * kDecodeWaves * 8 * kMergeStride <= 2 * sizeof(ChunkLds), "merge buffer exceeds the arena");
+    ChunkLds *bufs = reinterpret_cast<ChunkLds *>(arena);
+    auto merge_o = reinterpret_cast<float (*)[8][kMergeStride]>(arena);
     __shared__ float merge_m[kDecodeWaves][8], merge_l[kDecodeWaves][8];
     __shared__ float kscale[kMaxSplitTokens], vscale[kMaxSplitTokens];
-    __shared__ float red[kDecodeWaves], qmax[kDecodeWaves][8];
+    __shared__ float red[kDecodeWaves], qmax[4][8];
     __shared__ v4i qlds[4][64];    // INT8 query operands, [MFMA c][lane]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, qq = lane >> 4, head = n & 7;
     const bool lo_col = n >= 8;
     const uint32_t split = blockIdx.x, g = blockIdx.y, row = blockIdx.z;
     const uint32_t length = p.pos + row + 1;
-    const uint32_t split_tokens = p.split_blocks * kDecodeBlock;
+    const uint32_t split_tokens = p.split_chunks * kChunk;
     const uint32_t begin = split * split_tokens;
     const uint32_t end = min(length, begin + split_tokens);
-    const uint32_t nblocks = end > begin ? (end - begin + kDecodeBlock - 1) / kDecodeBlock : 0;
+    const uint32_t nchunks = end > begin ? (end - begin + kChunk - 1) / kChunk : 0;
 
     // ---- the small loads first (scales of the split, this wave's query chunk), then
-    // the first K/V block: waits on the memory counter are in order, so the set-up
-    // below never waits for the block
+    // the first two chunks: waits on the memory counter are in order, so the set-up
+    // below never waits for the chunks
     // (a fixed count of loads, no branches: the counter waits below stay exact;
     // indices past the split repeat its last token, a cache hit)
     const uint32_t last = (end > begin ? end : length) - 1;
-    float ksv[kMaxSplitTokens / 256], vsv[kMaxSplitTokens / 256];
+    float ksv[kMaxSplitTokens / 512], vsv[kMaxSplitTokens / 512];
 #pragma unroll
-    for (int it = 0; it < kMaxSplitTokens / 256; it++) {
-        const size_t at = (size_t)min(begin + tid + 256 * it, last) * 2 + g;
+    for (int it = 0; it < kMaxSplitTokens / 512; it++) {
+        const size_t at = (size_t)min(begin + tid + 512 * it, last) * 2 + g;
         ksv[it] = p.ks[at];
         vsv[it] = p.vs[at];
     }
-    // query chunk c = wave: lane (n, qq) takes dims 64c + 16qq + [0, 16) of head n % 8
+    // query chunk c = wave % 4: lane (n, qq) takes dims 64c + 16qq + [0, 16) of head
+    // n % 8 (waves 4-7 load the same chunks and only waves 0-3 publish them)
+    const int chunk = wave & 3;
     float4 x[4];
     {
-        const float *qh = p.q + ((size_t)row * 16 + g * 8 + head) * 256 + 64 * wave + 16 * qq;
+        const float *qh = p.q + ((size_t)row * 16 + g * 8 + head) * 256 + 64 * chunk + 16 * qq;
 #pragma unroll
         for (int f = 0; f < 4; f++) x[f] = *reinterpret_cast<const float4 *>(qh + 4 * f);
     }
-    // unconditional (a wave without blocks re-reads the first one, a cache hit): the
-    // counter waits stay exact
-    DecodeBlock cur, nxt;
-    load_block(cur, p, g, begin + ((uint32_t)wave < nblocks ? wave : 0) * kDecodeBlock, length, lane, n, qq);
+    // every wave's small loads enter the CU's memory pipeline before any chunk load
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    ChunkRegs r1, r2;
+    load_chunk(r2, p, g, begin, 0, nchunks, length, tid);
+    load_chunk(r1, p, g, begin, 1, nchunks, length, tid);
 
     // ---- scales of the split (this group) into LDS, vs_ref = their maximum; the
     // per-head maxima of the query chunks
     float vmax = 0.0f;
 #pragma unroll
-    for (int it = 0; it < kMaxSplitTokens / 256; it++) {
-        const uint32_t e = tid + 256 * it;   // < kMaxSplitTokens; entries past the split are never read
+    for (int it = 0; it < kMaxSplitTokens / 512; it++) {
+        const uint32_t e = tid + 512 * it;   // < kMaxSplitTokens; entries past the split are never read
         // masked by a multiply, not a select: every load above stays unconditional
         // (the clamped indices never reach a poisoned, non-finite tail scale)
         const float inside = begin + e < end ? 1.0f : 0.0f;
@@ -238,9 +287,11 @@ __global__ __launch_bounds__(256, 2) void decode_int8_kernel(DecodeParams p) {
     for (int f = 0; f < 4; f++) amax = fmaxf(amax, fmaxf(fmaxf(fabsf(x[f].x), fabsf(x[f].y)), fmaxf(fabsf(x[f].z), fabsf(x[f].w))));
     amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
     amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
-    if (lane < 8) qmax[wave][lane] = amax;
+    if (lane < 8 && wave < 4) qmax[wave][lane] = amax;
     __syncthreads();
-    const float vs_ref = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float vs_ref = red[0];
+#pragma unroll
+    for (int w = 1; w < kDecodeWaves; w++) vs_ref = fmaxf(vs_ref, red[w]);
     const float vs_inv = vs_ref > 0.0f ? 1.0f / vs_ref : 0.0f;
     // ---- INT8 query operand of chunk c = wave: part n / 8 of q ~= s_q (q1 + q2 / 254)
     const float qabs = fmaxf(fmaxf(qmax[0][head], qmax[1][head]), fmaxf(qmax[2][head], qmax[3][head]));
@@ -255,8 +306,12 @@ __global__ __launch_bounds__(256, 2) void decode_int8_kernel(DecodeParams p) {
         uint32_t w[4];
 #pragma unroll
         for (int f = 0; f < 4; f++) w[f] = part(x[f].x) | (part(x[f].y) << 8) | (part(x[f].z) << 16) | (part(x[f].w) << 24);
-        qlds[wave][lane] = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+        if (wave < 4) qlds[wave][lane] = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
     }
+    // chunk 0 into buffer 0 and chunk 2 into the registers it leaves: the loop
+    // below starts with r1 = chunk 1, r2 = chunk 2
+    store_chunk(bufs[0], r2, tid);
+    load_chunk(r2, p, g, begin, 2, nchunks, length, tid);
     __syncthreads();
     v4i qi[4];
 #pragma unroll
@@ -267,75 +322,89 @@ __global__ __launch_bounds__(256, 2) void decode_int8_kernel(DecodeParams p) {
     for (int i = 0; i < 16; i++) o[i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     float m = -INFINITY, l = 0.0f;
 
-    for (uint32_t b = wave; b < nblocks; b += kDecodeWaves) {
-        const uint32_t t0 = begin + b * kDecodeBlock;
-        const bool more = b + kDecodeWaves < nblocks;            // wave-uniform
-        // the last block re-reads itself (a cache hit) rather than branching
-        load_block(nxt, p, g, more ? t0 + kDecodeWaves * kDecodeBlock : t0, length, lane, n, qq);
-        v4i s[2];
-#pragma unroll
-        for (int a = 0; a < 2; a++) {
+    // one chunk from LDS: QK, the online softmax, PV
+    auto compute = [&](const ChunkLds &b, uint32_t c) {
+            const int tl = 16 * wave + (lane & 15);          // the lane's K row of the chunk
+            // S^T: rows = tokens 16w + 4qq + r of the chunk, columns n
             v4i acc = {0, 0, 0, 0};
-#pragma unroll
+    #pragma unroll
             for (int j = 0; j < 4; j++)
-                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, cur.k[a][j]), qi[j], acc, 0, 0, 0);
-            s[a] = acc;
-        }
-        // C layout: lane (n, qq) holds rows 4*qq + r -> token t0 + 8*qq + 4*a + r; the
-        // partner column n ^ 8 holds the other part of the same head.
-        const int local0 = (int)(t0 - begin) + 8 * qq;          // token offset inside the split
-        float sc[8];
-        float top = -INFINITY;
-#pragma unroll
-        for (int a = 0; a < 2; a++)
-#pragma unroll
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, b.k[tl][(4 * j + qq) ^ (tl & 15)]), qi[j], acc, 0, 0, 0);
+            // the partner column n ^ 8 holds the other part of the same head
+            const int local0 = (int)(c * kChunk) + 16 * wave + 4 * qq;   // token offset inside the split
+            const uint32_t t0 = begin + (uint32_t)local0;
+            float sc[4];
+            float top = -INFINITY;
+    #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int mine = s[a][r], other = __shfl_xor(mine, 8, 64);
+                const int mine = acc[r], other = __shfl_xor(mine, 8, 64);
                 const float full = ((float)(lo_col ? other : mine) + (float)(lo_col ? mine : other) * (1.0f / 254.0f)) * qsc;
-                const uint32_t t = t0 + 8 * qq + 4 * a + r;
-                const float value = t < end ? full * kscale[local0 + 4 * a + r] : -INFINITY;
-                sc[a * 4 + r] = value;
+                const float value = t0 + r < end ? full * kscale[local0 + r] : -INFINITY;
+                sc[r] = value;
                 top = fmaxf(top, value);
             }
-        top = fmaxf(top, __shfl_xor(top, 16, 64));
-        top = fmaxf(top, __shfl_xor(top, 32, 64));
-        const float next = fmaxf(m, top);
-        const float decay = __builtin_amdgcn_exp2f(m - next);
-        float total = 0.0f;
-        uint32_t pw[4];
-#pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-            _Float16 hv[2];
-#pragma unroll
-            for (int u = 0; u < 2; u++) {
-                const float prob = __builtin_amdgcn_exp2f(sc[e + u] - next);   // 0 for masked tokens
+            top = fmaxf(top, __shfl_xor(top, 16, 64));
+            top = fmaxf(top, __shfl_xor(top, 32, 64));
+            const float next = fmaxf(m, top);
+            // a wave whose tokens are all past the split end keeps m = -inf: no decay
+            const float decay = next == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - next);
+            float total = 0.0f;
+            _Float16 hv[4];
+    #pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float prob = next == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc[r] - next);   // 0 for masked tokens
                 total += prob;
-                const float scaled = prob * (vscale[local0 + e + u] * vs_inv);
+                const float scaled = prob * (vscale[local0 + r] * vs_inv);
                 const _Float16 hi = (_Float16)scaled;
-                hv[u] = lo_col ? (_Float16)(scaled - (float)hi) : hi;
+                hv[r] = lo_col ? (_Float16)(scaled - (float)hi) : hi;
             }
-            const half2v ph = {hv[0], hv[1]};
-            pw[e / 2] = __builtin_bit_cast(uint32_t, ph);
-        }
-        total += __shfl_xor(total, 16, 64);
-        total += __shfl_xor(total, 32, 64);
-        l = l * decay + total;
-        m = next;
-        if (decay != 1.0f) {
-#pragma unroll
-            for (int i = 0; i < 16; i++) o[i] *= decay;
-        }
-        const half8 pop = __builtin_bit_cast(half8, make_uint4(pw[0], pw[1], pw[2], pw[3]));
-#pragma unroll
-        for (int dt = 0; dt < 16; dt++)
-            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(i8x8_to_half8(cur.v[dt].x, cur.v[dt].y), pop, o[dt], 0, 0, 0);
-        // the copy waits for the prefetched block: keep it after this block's MFMAs
-        __builtin_amdgcn_sched_barrier(0);
-        cur = nxt;
+            total += __shfl_xor(total, 16, 64);
+            total += __shfl_xor(total, 32, 64);
+            l = l * decay + total;
+            m = next;
+            if (decay != 1.0f) {
+    #pragma unroll
+                for (int i = 0; i < 16; i++) o[i] *= decay;
+            }
+            const half4 pop = {hv[0], hv[1], hv[2], hv[3]};
+            // V^T operand: row d = 16dt + n, the 4 codes of tokens 16w + 4qq + [0, 4)
+            const int vpiece = wave;   // tokens 16w..16w+15
+    #pragma unroll
+            for (int dt = 0; dt < 16; dt++) {
+                const int d = 16 * dt + n;
+                const uint32_t w4 = reinterpret_cast<const uint32_t *>(&b.v[d][vpiece ^ ((d >> 1) & 7)])[qq];
+                uint32_t h0, h1;
+                i8x4_to_f16(w4, h0, h1);
+                const half4 va = __builtin_bit_cast(half4, make_uint2(h0, h1));
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pop, o[dt], 0, 0, 0);
+            }
+    };
+    // Chunks in pairs, so that the two register sets take turns without copies (a
+    // copy of registers still being loaded waits for the load). At the top of a
+    // pair: buffer 0 holds chunk c, r1 chunk c + 1, r2 chunk c + 2. The odd tail only
+    // skips a compute; the loads and barriers stay unconditional. (A third register
+    // set, three chunks in flight, measured slower: the longer start-up burst delays
+    // every work-group's first chunk.)
+    for (uint32_t c = 0; c < nchunks; c += 2) {
+        compute(bufs[0], c);
+        store_chunk(bufs[1], r1, tid);   // buffer 1's chunk c - 1 was finished before the last barrier
+        load_chunk(r1, p, g, begin, c + 3, nchunks, length, tid);
+        __syncthreads();
+        if (c + 1 < nchunks) compute(bufs[1], c + 1);
+        store_chunk(bufs[0], r2, tid);
+        load_chunk(r2, p, g, begin, c + 4, nchunks, length, tid);
+        __syncthreads();
     }
 
-    // ---- merge the four waves: O^T[d][n] with d = 16*dt + 4*qq + r; heads sum hi + lo columns;
-    // statistics are in base 2, O in units of vs_ref.
+    // ---- merge the eight waves: O^T[d][n] with d = 16*dt + 4*qq + r; heads sum hi + lo columns;
+    // statistics are in base 2, O in units of vs_ref. The arena is free: the loop
+    // ended with a barrier and no chunk is read again.
+    // the lo column n + 8 of each head joins its hi column n in registers (a lane
+    // swap inside each 16-lane row), then the hi lanes publish the head
+#pragma unroll
+    for (int dt = 0; dt < 16; dt++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) o[dt][r] += __shfl_xor(o[dt][r], 8, 64);
     if (n < 8) {
 #pragma unroll
         for (int dt = 0; dt < 16; dt++)
@@ -346,13 +415,8 @@ __global__ __launch_bounds__(256, 2) void decode_int8_kernel(DecodeParams p) {
         }
     }
     __syncthreads();
-    if (n >= 8) {
-#pragma unroll
-        for (int dt = 0; dt < 16; dt++) *reinterpret_cast<floatx4 *>(&merge_o[wave][head][16 * dt + 4 * qq]) += o[dt];
-    }
-    __syncthreads();
-    // thread -> (head h, 8 dims); combine waves with their maxima
-    const int h = threadIdx.x >> 5, d0 = (threadIdx.x & 31) * 8;
+    // thread -> (head h, 4 dims); combine waves with their maxima
+    const int h = threadIdx.x >> 6, d0 = (threadIdx.x & 63) * 4;
     float mw = -INFINITY;
     for (int w = 0; w < kDecodeWaves; w++) mw = fmaxf(mw, merge_m[w][h]);
     float lw = 0.0f, f[kDecodeWaves];
@@ -360,21 +424,31 @@ __global__ __launch_bounds__(256, 2) void decode_int8_kernel(DecodeParams p) {
         f[w] = merge_m[w][h] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(merge_m[w][h] - mw);
         lw += merge_l[w][h] * f[w];
     }
-    float acc[8];
-    for (int e = 0; e < 8; e++) {
-        float sum = 0.0f;
-        for (int w = 0; w < kDecodeWaves; w++) sum += merge_o[w][h][d0 + e] * f[w];
-        acc[e] = sum * vs_ref;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int w = 0; w < kDecodeWaves; w++) {
+        const float4 ow = *reinterpret_cast<const float4 *>(&merge_o[w][h][d0]);
+        acc.x += ow.x * f[w];
+        acc.y += ow.y * f[w];
+        acc.z += ow.z * f[w];
+        acc.w += ow.w * f[w];
     }
+    acc.x *= vs_ref;
+    acc.y *= vs_ref;
+    acc.z *= vs_ref;
+    acc.w *= vs_ref;
     if (p.splits == 1) {
+        // gate and y need only 4-byte alignment
         const size_t at = ((size_t)row * 16 + g * 8 + h) * 256 + d0;
-        for (int e = 0; e < 8; e++) p.y[at + e] = acc[e] / lw * sigmoidf(p.gate[at + e]);
+        const float inv = 1.0f / lw;
+        p.y[at + 0] = acc.x * inv * sigmoidf(p.gate[at + 0]);
+        p.y[at + 1] = acc.y * inv * sigmoidf(p.gate[at + 1]);
+        p.y[at + 2] = acc.z * inv * sigmoidf(p.gate[at + 2]);
+        p.y[at + 3] = acc.w * inv * sigmoidf(p.gate[at + 3]);
         return;
     }
     float *part = p.partial + (((size_t)row * 2 + g) * p.splits + split) * kPartialFloats;
-    *reinterpret_cast<float4 *>(part + h * 256 + d0) = make_float4(acc[0], acc[1], acc[2], acc[3]);
-    *reinterpret_cast<float4 *>(part + h * 256 + d0 + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
-    if ((threadIdx.x & 31) == 0) {
+    *reinterpret_cast<float4 *>(part + h * 256 + d0) = acc;
+    if ((threadIdx.x & 63) == 0) {
         part[2048 + h] = mw;
         part[2056 + h] = lw;
     }
@@ -545,15 +619,14 @@ const char *launch_decode_int8(Context &c, const View *b, int count, const boot_
     BOOT_REQUIRE(aligned(b[0].ptr, 16) && aligned(b[1].ptr, 16) && aligned(b[2].ptr, 16) && aligned(b[3].ptr, 4) &&
                      aligned(b[4].ptr, 4) && aligned(b[5].ptr, 4) && aligned(b[6].ptr, 4),
                  "bindings misaligned (q, k, v need 16 bytes)");
-    // Split length in 32-token blocks, chosen so that the grid (splits x 2 groups x
-    // rows, two work-groups per CU) fits the CUs in one round: a second, nearly empty
+    // Split length in 128-token chunks, chosen so that the grid (splits x 2 groups x
+    // rows, one work-group per CU) fits the CUs in one round: a second, nearly empty
     // round would double the time. At most kMaxSplitTokens per split.
-    const uint64_t total_blocks = (length + kDecodeBlock - 1) / kDecodeBlock;
-    const uint64_t slots = std::max<uint64_t>(1, 2ull * (uint64_t)std::max(1, context_cus(c)) / (2 * rows));
-    uint64_t split_blocks = (total_blocks + slots - 1) / slots;
-    split_blocks = std::max<uint64_t>(split_blocks, (uint64_t)kDecodeWaves);             // one block per wave at least
-    split_blocks = std::min<uint64_t>(split_blocks, (uint64_t)(kMaxSplitTokens / kDecodeBlock));
-    const uint64_t splits = (total_blocks + split_blocks - 1) / split_blocks;
+    const uint64_t total_chunks = (length + kChunk - 1) / kChunk;
+    const uint64_t slots = std::max<uint64_t>(1, (uint64_t)std::max(1, context_cus(c)) / (2 * rows));
+    uint64_t split_chunks = (total_chunks + slots - 1) / slots;
+    split_chunks = std::min<uint64_t>(split_chunks, (uint64_t)(kMaxSplitTokens / kChunk));
+    const uint64_t splits = (total_chunks + split_chunks - 1) / split_chunks;
     BOOT_REQUIRE(splits <= kMaxDecodeSplits, "too many decode splits");
     DecodeParams d;
     d.q = (const float *)b[0].ptr;
@@ -566,13 +639,13 @@ const char *launch_decode_int8(Context &c, const View *b, int count, const boot_
     d.rows = (uint32_t)rows;
     d.pos = p.pos;
     d.splits = (uint32_t)splits;
-    d.split_blocks = (uint32_t)split_blocks;
+    d.split_chunks = (uint32_t)split_chunks;
     d.partial = nullptr;
     if (splits > 1) {
         d.partial = (float *)context_workspace(c, rows * 2 * splits * kPartialFloats * sizeof(float));
         BOOT_REQUIRE(d.partial, "cannot allocate decode split workspace");
     }
-    decode_int8_kernel<<<dim3((uint32_t)splits, 2, (uint32_t)rows), 256, 0, context_stream(c)>>>(d);
+    decode_int8_kernel<<<dim3((uint32_t)splits, 2, (uint32_t)rows), 512, 0, context_stream(c)>>>(d);
     if (splits > 1) {
         context_split(c, "attention_decode_int8.combine");
         decode_combine_kernel<<<dim3(4, 16, (uint32_t)rows), 256, 0, context_stream(c)>>>(d.partial, d.gate, d.y,

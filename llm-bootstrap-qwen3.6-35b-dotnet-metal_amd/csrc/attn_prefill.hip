@@ -586,29 +586,17 @@ __global__ __launch_bounds__(512, 1) void prefill_pp_kernel(PrefillParams p) {
                     }
                 }
             } else if (n < ntiles) {
-                // ---- VALU work: staging of tile n+1 and the prefetch of tile n+2 first
-                // (their registers are free again before the softmax needs its own),
-                // then the online softmax of tile n (lane value v is key
-                // key0 + 16(v/8) + 8kk + v%8)
+                // ---- VALU work: the online softmax of tile n (lane value v is key
+                // key0 + 16(v/8) + 8kk + v%8), then the staging of tile n+1 and the
+                // prefetch of tile n+2. Staged last, the LDS writes (queued behind the
+                // other team's operand reads) complete while this wave waits at the
+                // barrier instead of delaying the softmax's scale reads.
                 const uint32_t key0 = kbeg + (uint32_t)n * kPPKeys;
                 const PPTile &b = buf[n & 1];
-                // K scales of the lane's keys first: their LDS latency overlaps the staging
                 float4 k4[4];
 #pragma unroll
                 for (int q4 = 0; q4 < 4; q4++)
                     k4[q4] = *reinterpret_cast<const float4 *>(b.ks + 16 * (q4 >> 1) + 8 * kk + 4 * (q4 & 1));
-                if (n + 1 < ntiles) {
-                    // tile n+1: team 0 writes K and the scales (buffer last read in slot
-                    // 2n - 1, scales in slot 2n), team 1 writes V (last read in slot 2n + 1)
-                    PPTile &nb = buf[(n + 1) & 1];
-#pragma unroll
-                    for (int q = 0; q < 4; q++) *quad_dst(nb, q) = convert_quad(q);
-                    store_scales(nb, key0 + kPPKeys);
-                    if (n + 2 < ntiles) {
-                        load_raw(key0 + 2 * kPPKeys);
-                        load_scales(key0 + 2 * kPPKeys);
-                    }
-                }
                 const float mref = m == -INFINITY ? 0.0f : m;
 #pragma unroll
                 for (int q4 = 0; q4 < 4; q4++) {
@@ -657,6 +645,18 @@ __global__ __launch_bounds__(512, 1) void prefill_pp_kernel(PrefillParams p) {
                     pb[u][e + 3] = (_Float16)(e3 * v4.w);
                 }
                 l += lsum;
+                if (n + 1 < ntiles) {
+                    // tile n+1: team 0 writes K and the scales (buffer last read in slot
+                    // 2n - 1, scales in slot 2n), team 1 writes V (last read in slot 2n + 1)
+                    PPTile &nb = buf[(n + 1) & 1];
+#pragma unroll
+                    for (int q = 0; q < 4; q++) *quad_dst(nb, q) = convert_quad(q);
+                    store_scales(nb, key0 + kPPKeys);
+                    if (n + 2 < ntiles) {
+                        load_raw(key0 + 2 * kPPKeys);
+                        load_scales(key0 + 2 * kPPKeys);
+                    }
+                }
             }
         }
         __syncthreads();
