@@ -173,12 +173,17 @@ def cpu_baseline_prefill(work: PrefillWorkload, threads: int):
 # --------------------------------------------------------------------------- decode
 
 class DecodeWorkload:
-    def __init__(self, device, context=131072, steps=256, seed=1, fill_chunk=8192):
+    """Config 4: single-token decode at 131072 context over the model's 10 full-attention
+    layers (QwenEngine.cs:161-165 per layer): each step appends one token to every layer and
+    attends over it. Ten layers of 136 MB do not fit the 256 MB last-level cache, so every
+    layer's K/V comes from HBM as it does in the model (re-reading a single layer would be
+    served partly from that cache)."""
+
+    def __init__(self, device, context=131072, steps=256, layers=10, seed=1, fill_chunk=8192):
         self.device, self.context, self.steps = device, context, steps
         rng = np.random.default_rng(seed)
-        self.cache = engine.Int8KvCache(device, context_window=engine.NATIVE_WINDOW, layers=1)
-        log(f"decode: filling {context} tokens (capacity grows by doubling from {self.cache.capacity})")
-        self.append_ms = 0.0
+        self.cache = engine.Int8KvCache(device, context_window=engine.NATIVE_WINDOW, layers=layers)
+        log(f"decode: filling {layers} layers x {context} tokens (capacity grows by doubling from {self.cache.capacity})")
         k_all = synthetic(rng, (context + steps, 2, 256), outliers=True)
         v_all = synthetic(rng, (context + steps, 2, 256))
         kb, vb = upload(device, k_all[:fill_chunk]), upload(device, v_all[:fill_chunk])
@@ -187,13 +192,14 @@ class DecodeWorkload:
             kb.write(k_all[pos:pos + fill_chunk])
             vb.write(v_all[pos:pos + fill_chunk])
             device.begin()
-            engine.store_rows(device, self.cache.layers[0], kb, vb, fill_chunk, pos)
+            for layer in self.cache.layers:                    # the same rows in every layer
+                engine.store_rows(device, layer, kb, vb, fill_chunk, pos)
             device.end()
-        self.cache.ensure_capacity(context + 1)                # pre-grow to 262144 before timing
+        self.cache.ensure_capacity(context + steps)            # pre-grow to 262144 before timing
         self.growth = list(self.cache.growth_log)
         kb.dispose()
         vb.dispose()
-        # one bulk append of the whole history into a second layer: the append roofline sample
+        # one bulk append of the whole history into another layer: the append roofline sample
         self.bulk_k = upload(device, k_all[:context])
         self.bulk_v = upload(device, v_all[:context])
         self.bulk_layer = engine.Int8KvLayer(device, context)
@@ -203,16 +209,20 @@ class DecodeWorkload:
         self.gate = upload(device, synthetic(rng, (steps, 16, 256)))
         self.rotated = device.allocate(steps * 16384)
         self.out = device.allocate(steps * 16384)
+        self.pos0 = context
 
     def run(self):
-        d, layer = self.device, self.cache.layers[0]
+        """One command of `steps` tokens; each token appends to and attends over every layer.
+        The positions advance from run to run (capacity was grown for all of them)."""
+        d = self.device
         d.begin()
         for i in range(self.steps):
-            pos = self.context + i
-            engine.append_rows(d, layer, self.q.at(i * 16384), self.k_new.at(i * 2048), self.v_new.at(i * 2048),
-                               self.rotated.at(i * 16384), 1, pos)
-            engine.decode(d, layer, self.rotated.at(i * 16384), self.gate.at(i * 16384), self.out.at(i * 16384),
-                          pos)
+            pos = self.pos0 + i
+            for layer in self.cache.layers:
+                engine.append_rows(d, layer, self.q.at(i * 16384), self.k_new.at(i * 2048), self.v_new.at(i * 2048),
+                                   self.rotated.at(i * 16384), 1, pos)
+                engine.decode(d, layer, self.rotated.at(i * 16384), self.gate.at(i * 16384), self.out.at(i * 16384),
+                              pos)
         d.end()
 
     def bulk_append(self):
@@ -222,8 +232,8 @@ class DecodeWorkload:
         d.end()
 
     def kv_bytes(self):
-        # 1040 B per attended token: 512 K + 512 V codes + 8 + 8 scale bytes (both KV heads)
-        return sum(1040 * (self.context + i + 1) for i in range(self.steps))
+        # 1040 B per attended token and layer: 512 K + 512 V codes + 8 + 8 scale bytes (both KV heads)
+        return len(self.cache.layers) * sum(1040 * (self.pos0 + i + 1) for i in range(self.steps))
 
 
 def main():
@@ -234,6 +244,12 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
+    ap.add_argument("--decode-steps", type=int, default=256,
+                    help="decode tokens per timed run (each over every layer); the counter runs "
+                         "of the profiles use fewer: traffic per launch does not depend on it")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run three 1 GiB device-to-device copies (boot_copy): the known-size "
+                         "reference that scales rocprofv3 FETCH_SIZE / WRITE_SIZE into bytes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is design-only (DESIGN.md)",
@@ -241,24 +257,50 @@ def main():
         sys.exit(2)
 
     device = Device()
+    if args.copy_probe:
+        n = 1 << 30
+        a, b = device.allocate(n), device.allocate(n)
+        for _ in range(3):
+            device.copy(b, 0, a, 0, n)
+        print(json.dumps({"copy_probe_bytes": n, "copies": 3}), flush=True)
+        device.close()
+        return
+    # ---- uninstrumented timed loops first: once wall accounting is reset (below), it
+    # stays on for the rest of the context's life
     work = PrefillWorkload(device)
     for _ in range(args.warmup):
         work.step()
-    # timed region: HIP events only around the attention kernels (the roofline's
-    # durations); each step ends with the library's stream synchronized (boot_end)
-    device.reset_wall_timing(sample_attention=True)
+    # each step ends with the library's stream synchronized (boot_end)
     t0 = time.perf_counter()
     for _ in range(args.steps):
         work.step()
     wall_ms = (time.perf_counter() - t0) * 1000.0 / args.steps
-    ks = kernel_stats(device, ["attention_online_int8_q32_k256_r2", "attention_online_int8.combine"])
-    attn_ms = ks["attention_online_int8_q32_k256_r2"][0] / args.steps
-    combine_ms = ks.get("attention_online_int8.combine", (0.0, 0))[0] / args.steps
-    launches = ks["attention_online_int8_q32_k256_r2"][1] // args.steps
-    # one more step with events around every kernel for the breakdown (not timed)
-    device.reset_wall_timing(all_kernels=True)
-    work.step()
-    ks.update(kernel_stats(device, ["batch_rope_int8", "attention_query_grouped_half"]))
+    control = Fp16ControlWorkload(work)
+    for _ in range(args.warmup):
+        control.step()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        control.step()
+    fp16_ms = (time.perf_counter() - t0) * 1000.0 / args.steps
+    dec = None
+    if not args.no_decode:
+        dec = DecodeWorkload(device, steps=args.decode_steps)
+        dec.run()  # warm (the positions are re-appended: the cache bytes are the same)
+        t0 = time.perf_counter()
+        dec.run()
+        dec_wall = (time.perf_counter() - t0) * 1000.0 / dec.steps
+        dec.bulk_append()
+
+    # ---- the same work again with every kernel of the path timed by events stamped
+    # from its own dispatch (no marker packets on the stream): the roofline's durations
+    device.reset_wall_timing(kernels_exact=True)
+    for _ in range(args.steps):
+        work.step()
+    ks = kernel_stats(device, ["prefill_pp_kernel", "prefill_combine_kernel<256>", "batch_rope_int8_kernel",
+                               "query_grouped_half_kernel"])
+    attn_ms = ks["prefill_pp_kernel"][0] / args.steps
+    combine_ms = ks.get("prefill_combine_kernel<256>", (0.0, 0))[0] / args.steps
+    launches = ks["prefill_pp_kernel"][1] // args.steps
     flops = work.flops()
     achieved = flops / (attn_ms * 1e-3) / 1e12
     result = {
@@ -270,66 +312,52 @@ def main():
                    "kv": "int8 + fp32 per-token/head scales", "tokens": 30720, "chunk": 512,
                    "parallelism": "single GPU"},
         "prefill": {"attention_kernel_ms_per_layer": round(attn_ms, 4), "combine_ms_per_layer": round(combine_ms, 4),
-                    "append_ms_per_layer": round(ks["batch_rope_int8"][0], 4),
-                    "query_pack_ms_per_layer": round(ks["attention_query_grouped_half"][0], 4),
+                    "append_ms_per_layer": round(ks["batch_rope_int8_kernel"][0] / args.steps, 4),
+                    "query_pack_ms_per_layer": round(ks["query_grouped_half_kernel"][0] / args.steps, 4),
                     "attention_launches_per_layer": launches,
                     "mfma_fraction_end_to_end": round(flops / (wall_ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4)},
-        "roofline": {"bound": "mfma", "kernel": "prefill_int8_kernel (attention_online_int8_q32_k256_r2)",
+        "roofline": {"bound": "mfma", "kernel": "prefill_pp_kernel (attention_online_int8_q32_k256_r2)",
                      "achieved": round(achieved, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / MFMA_PEAK_TFLOPS, 4),
-                     "traffic": measured_traffic("prefill_kernel<true>"),
+                     "traffic": measured_traffic("prefill_pp_kernel"),
                      "flops_per_layer": flops},
     }
-    control = Fp16ControlWorkload(work)
-    for _ in range(args.warmup):
-        control.step()
-    device.reset_wall_timing(sample_attention=True)
-    t0 = time.perf_counter()
+    device.reset_wall_timing(kernels_exact=True)
     for _ in range(args.steps):
         control.step()
-    fp16_ms = (time.perf_counter() - t0) * 1000.0 / args.steps
-    kc = kernel_stats(device, ["attention_online_q32_k256_s8_g8_r2", "attention_online_fp16.combine"])
-    device.reset_wall_timing(all_kernels=True)
-    control.step()
-    kc.update(kernel_stats(device, ["batch_rope"]))
+    kc = kernel_stats(device, ["prefill_kernel<false>", "prefill_combine_kernel<128>", "batch_rope_half_kernel"])
     result["fp16_kv_control"] = {
         "ms_per_layer": round(fp16_ms, 4),
-        "attention_kernel_ms_per_layer": round(kc["attention_online_q32_k256_s8_g8_r2"][0] / args.steps, 4),
-        "combine_ms_per_layer": round(kc.get("attention_online_fp16.combine", (0.0, 0))[0] / args.steps, 4),
-        "append_ms_per_layer": round(kc["batch_rope"][0], 4),
+        "attention_kernel_ms_per_layer": round(kc["prefill_kernel<false>"][0] / args.steps, 4),
+        "combine_ms_per_layer": round(kc.get("prefill_combine_kernel<128>", (0.0, 0))[0] / args.steps, 4),
+        "append_ms_per_layer": round(kc["batch_rope_half_kernel"][0] / args.steps, 4),
         "int8_over_fp16_time": round(wall_ms / fp16_ms, 4),
         "kv_bytes_30k": {"int8_with_scales": 30720 * 1040, "fp16": 30720 * 2048}}
-    if not args.no_decode:
-        dec = DecodeWorkload(device)
-        dec.run()  # warm
-        device.reset_wall_timing(sample_attention=True)
-        t0 = time.perf_counter()
+    if dec is not None:
+        device.reset_wall_timing(kernels_exact=True)
         dec.run()
-        dec_wall = (time.perf_counter() - t0) * 1000.0 / dec.steps
-        kd = kernel_stats(device, ["attention_decode_int8", "attention_decode_int8.combine"])
-        dec_kernel_ms = kd["attention_decode_int8"][0] / dec.steps
-        dec_comb_ms = kd.get("attention_decode_int8.combine", (0.0, 0))[0] / dec.steps
-        device.reset_wall_timing(all_kernels=True)   # append breakdown, not timed
-        dec.run()
-        append_ms = kernel_stats(device, ["batch_rope_int8"])["batch_rope_int8"][0] / dec.steps
-        bytes_per_step = dec.kv_bytes() / dec.steps
+        kd = kernel_stats(device, ["decode_int8_kernel", "decode_combine_kernel", "batch_rope_int8_kernel"])
+        dispatches = dec.steps * len(dec.cache.layers)
+        dec_kernel_ms = kd["decode_int8_kernel"][0] / dispatches
+        dec_comb_ms = kd.get("decode_combine_kernel", (0.0, 0))[0] / dispatches
+        append_ms = kd["batch_rope_int8_kernel"][0] / dispatches
+        bytes_per_dispatch = dec.kv_bytes() / dispatches
+        device.reset_wall_timing(kernels_exact=True)
         dec.bulk_append()
-        device.reset_wall_timing(all_kernels=True)
-        dec.bulk_append()
-        bulk = kernel_stats(device, ["kv_store_int8"])["kv_store_int8"][0]
+        bulk = kernel_stats(device, ["kv_store_int8_kernel"])["kv_store_int8_kernel"][0]
         bulk_bytes = 5136.0 * dec.context
         result["decode"] = {
-            "context": dec.context, "steps": dec.steps, "growth": dec.growth,
-            "kv_read_gbs_step": round(bytes_per_step / (dec_wall * 1e-3) / 1e9, 1),
-            "kv_read_gbs_attention_kernels": round(bytes_per_step / ((dec_kernel_ms + dec_comb_ms) * 1e-3) / 1e9, 1),
-            "ms_per_step_wall": round(dec_wall, 5), "decode_kernel_us": round(dec_kernel_ms * 1000, 3),
+            "context": dec.context, "layers": len(dec.cache.layers), "steps": dec.steps, "growth": dec.growth,
+            "kv_read_gbs_step": round(dec.kv_bytes() / dec.steps / (dec_wall * 1e-3) / 1e9, 1),
+            "kv_read_gbs_attention_kernels": round(bytes_per_dispatch / ((dec_kernel_ms + dec_comb_ms) * 1e-3) / 1e9, 1),
+            "ms_per_token_step_wall": round(dec_wall, 5), "decode_kernel_us": round(dec_kernel_ms * 1000, 3),
             "combine_kernel_us": round(dec_comb_ms * 1000, 3), "append_kernel_us": round(append_ms * 1000, 3),
-            "bytes_per_step": bytes_per_step,
+            "bytes_per_layer_step": bytes_per_dispatch,
         }
         result["roofline_decode"] = {
             "bound": "hbm", "kernel": "decode_int8_kernel (attention_decode_int8)",
-            "achieved": round(bytes_per_step / (dec_kernel_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(bytes_per_step / (dec_kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "achieved": round(bytes_per_dispatch / (dec_kernel_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(bytes_per_dispatch / (dec_kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic("decode_int8_kernel")}
         result["roofline_append"] = {
             "bound": "hbm", "kernel": "kv_store_int8 bulk append of 131072 tokens",

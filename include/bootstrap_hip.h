@@ -73,7 +73,9 @@ int boot_end(void *ctx);
 /* bridge.mm:70. Serialized per-dispatch timing (BOOTSTRAP_PROFILE equivalent). */
 void boot_profile(void *ctx, int enabled);
 /* bridge.mm:71-94. Resets wall accounting; sample_attention 1 samples the
- * attention kernels, 2 every kernel, with HIP events on the context stream. */
+ * attention kernels, 2 every kernel, with HIP events on the context stream,
+ * keyed by dispatch name; 3 times each kernel of the path alone, keyed by kernel
+ * function, with events stamped by its own dispatch (no marker packets). */
 int boot_wall_reset(void *ctx, int sample_attention);
 /* bridge.mm:95-105. wall[7] = {gpu s, encode s, commit s, wait s, commands,
  * dispatches, resolve s}; attention[6] = {qk s, softmax s, av s, counts x3}. */

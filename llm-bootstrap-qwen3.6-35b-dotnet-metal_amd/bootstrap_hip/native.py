@@ -164,8 +164,12 @@ class Device:
     def set_profiling(self, enabled: bool) -> None:
         self.lib.boot_profile(self.handle, 1 if enabled else 0)
 
-    def reset_wall_timing(self, sample_attention: bool = False, all_kernels: bool = False) -> None:
-        self._check(self.lib.boot_wall_reset(self.handle, 2 if all_kernels else 1 if sample_attention else 0))
+    def reset_wall_timing(self, sample_attention: bool = False, all_kernels: bool = False,
+                          kernels_exact: bool = False) -> None:
+        """Metal.cs:84 (ResetWallTiming). ``kernels_exact`` times each kernel of the path by
+        itself, keyed by kernel function, with events stamped by its own dispatch."""
+        mode = 3 if kernels_exact else 2 if all_kernels else 1 if sample_attention else 0
+        self._check(self.lib.boot_wall_reset(self.handle, mode))
 
     def read_wall_timing(self) -> dict:
         """Metal.cs:84-92."""

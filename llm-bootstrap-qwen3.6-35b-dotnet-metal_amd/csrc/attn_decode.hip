@@ -645,11 +645,11 @@ const char *launch_decode_int8(Context &c, const View *b, int count, const boot_
         d.partial = (float *)context_workspace(c, rows * 2 * splits * kPartialFloats * sizeof(float));
         BOOT_REQUIRE(d.partial, "cannot allocate decode split workspace");
     }
-    decode_int8_kernel<<<dim3((uint32_t)splits, 2, (uint32_t)rows), 512, 0, context_stream(c)>>>(d);
+    launch_timed(c, "decode_int8_kernel", decode_int8_kernel, dim3((uint32_t)splits, 2, (uint32_t)rows), dim3(512), d);
     if (splits > 1) {
         context_split(c, "attention_decode_int8.combine");
-        decode_combine_kernel<<<dim3(4, 16, (uint32_t)rows), 256, 0, context_stream(c)>>>(d.partial, d.gate, d.y,
-                                                                                        (uint32_t)splits);
+        launch_timed(c, "decode_combine_kernel", decode_combine_kernel, dim3(4, 16, (uint32_t)rows), dim3(256), d.partial,
+                     d.gate, d.y, (uint32_t)splits);
     }
     return nullptr;
 }

@@ -814,15 +814,15 @@ const char *launch_prefill(Context &c, const View *b, int count, const boot_kern
         BOOT_REQUIRE(p.partial, "cannot allocate prefill split workspace");
     }
     if (int8)
-        prefill_pp_kernel<<<(uint32_t)blocks, 512, 0, context_stream(c)>>>(p);
+        launch_timed(c, "prefill_pp_kernel", prefill_pp_kernel, dim3((uint32_t)blocks), dim3(512), p);
     else
-        prefill_kernel<false><<<(uint32_t)blocks, 256, 0, context_stream(c)>>>(p);
+        launch_timed(c, "prefill_kernel<false>", prefill_kernel<false>, dim3((uint32_t)blocks), dim3(256), p);
     if (splits > 1) {
         context_split(c, int8 ? "attention_online_int8.combine" : "attention_online_fp16.combine");
         if (int8)
-            prefill_combine_kernel<kPPRows><<<dim3(kPPRows / 4, p.tiles, 2), 256, 0, context_stream(c)>>>(p);
+            launch_timed(c, "prefill_combine_kernel<256>", prefill_combine_kernel<kPPRows>, dim3(kPPRows / 4, p.tiles, 2), dim3(256), p);
         else
-            prefill_combine_kernel<kRows><<<dim3(kRows / 4, p.tiles, 2), 256, 0, context_stream(c)>>>(p);
+            launch_timed(c, "prefill_combine_kernel<128>", prefill_combine_kernel<kRows>, dim3(kRows / 4, p.tiles, 2), dim3(256), p);
     }
     return nullptr;
 }

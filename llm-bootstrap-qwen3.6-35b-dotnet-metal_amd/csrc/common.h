@@ -1,5 +1,6 @@
 // Shared host/device declarations of libbootstrap_hip.so (gfx950 only).
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -42,6 +43,25 @@ int context_cus(Context &c);
 // Ends the current timing sample of a multi-kernel dispatch and starts one
 // named `name` (no-op unless kernel sampling is on).
 void context_split(Context &c, const char *name);
+// Kernel-exact timing: in that wall-timing mode, returns start/stop events for
+// hipExtLaunchKernelGGL, which stamps them from the dispatch packet itself (no
+// marker packets on the stream), and records them as a sample named `kernel`;
+// otherwise returns null events.
+void context_kernel_events(Context &c, const char *kernel, hipEvent_t *start, hipEvent_t *stop);
+
+// Enqueues `f` on the context stream, through hipExtLaunchKernelGGL with
+// kernel-exact events when that mode is on (a slower host path), else as a plain
+// launch. The arguments are converted to the kernel's parameter types first: the
+// extended launch packs them by the types it is given.
+template <typename... Params, typename... Args>
+inline void launch_timed(Context &c, const char *kernel, void (*f)(Params...), dim3 grid, dim3 block, Args... args) {
+    hipEvent_t start = nullptr, stop = nullptr;
+    context_kernel_events(c, kernel, &start, &stop);
+    if (start)
+        hipExtLaunchKernelGGL(f, grid, block, 0, context_stream(c), start, stop, 0, static_cast<Params>(args)...);
+    else
+        f<<<grid, block, 0, context_stream(c)>>>(static_cast<Params>(args)...);
+}
 
 // Byte offset of the V code for (vector = token*2 + head, dimension d).
 // kernels.metal:126-128 (int8_value_index).

@@ -381,7 +381,7 @@ const char *launch_kv_store_int8(Context &c, const View *b, int count, const boo
     if (const char *e = check_cache(b, 2, 3, 4, 5, end)) return e;
     const uint32_t first = p.pos / kTile, last = (uint32_t)((end - 1) / kTile);
     const uint32_t blocks = (last - first + 1) * 2;
-    kv_store_int8_kernel<<<blocks, 256, 0, context_stream(c)>>>(
+    launch_timed(c, "kv_store_int8_kernel", kv_store_int8_kernel, dim3(blocks), dim3(256), 
         (const float *)b[0].ptr, (const float *)b[1].ptr, (int8_t *)b[2].ptr, (int8_t *)b[3].ptr,
         (float *)b[4].ptr, (float *)b[5].ptr, (uint32_t)rows, p.pos, first);
     return nullptr;
@@ -401,7 +401,7 @@ const char *launch_batch_rope_int8(Context &c, const View *b, int count, const b
     const uint32_t qblocks = (uint32_t)((rows + 3) / 4);
     const uint32_t first = p.pos / kTile, last = (uint32_t)((end - 1) / kTile);
     const uint32_t blocks = qblocks + (last - first + 1) * 2;
-    batch_rope_int8_kernel<<<blocks, 256, 0, context_stream(c)>>>(
+    launch_timed(c, "batch_rope_int8_kernel", batch_rope_int8_kernel, dim3(blocks), dim3(256), 
         (const float *)b[0].ptr, (const float *)b[1].ptr, (const float *)b[2].ptr, (float *)b[3].ptr,
         (int8_t *)b[4].ptr, (int8_t *)b[5].ptr, (float *)b[6].ptr, (float *)b[7].ptr, (uint32_t)rows,
         p.pos, p.theta, qblocks, first);
@@ -419,7 +419,7 @@ const char *launch_query_grouped_half(Context &c, const View *b, int count, cons
     BOOT_REQUIRE(rows <= 262144, "rows exceed the 262144-token window");
     BOOT_REQUIRE(aligned(b[0].ptr, 16) && aligned(b[1].ptr, 16), "query bindings must be 16-byte aligned");
     const uint64_t threads = rows * 512;
-    query_grouped_half_kernel<<<(uint32_t)((threads + 255) / 256), 256, 0, context_stream(c)>>>(
+    launch_timed(c, "query_grouped_half_kernel", query_grouped_half_kernel, dim3((uint32_t)((threads + 255) / 256)), dim3(256), 
         (const float *)b[0].ptr, (_Float16 *)b[1].ptr, (uint32_t)rows, (uint32_t)__builtin_ctz(p.a));
     return nullptr;
 }
@@ -441,7 +441,7 @@ const char *launch_prepare_fused_int8(Context &c, const View *b, int count, cons
     if (const char *e = check_cache(b, 7, 8, 9, 10, end)) return e;
     const uint32_t qblocks = (uint32_t)((rows + 3) / 4);
     const uint32_t first = p.pos / kTile, last = (uint32_t)((end - 1) / kTile);
-    prepare_fused_int8_kernel<<<qblocks + (last - first + 1) * 2, 256, 0, context_stream(c)>>>(
+    launch_timed(c, "prepare_fused_int8_kernel", prepare_fused_int8_kernel, dim3(qblocks + (last - first + 1) * 2), dim3(256), 
         (const float *)b[0].ptr, (const float *)b[1].ptr, (const float *)b[2].ptr, (const uint16_t *)b[3].ptr,
         (const uint16_t *)b[4].ptr, (_Float16 *)b[5].ptr, (float *)b[6].ptr, (int8_t *)b[7].ptr, (int8_t *)b[8].ptr,
         (float *)b[9].ptr, (float *)b[10].ptr, (uint32_t)rows, p.pos, p.theta, p.eps, qblocks, first);
@@ -460,7 +460,7 @@ const char *launch_batch_rope_half(Context &c, const View *b, int count, const b
     BOOT_REQUIRE(aligned(b[0].ptr, 16) && aligned(b[1].ptr, 16) && aligned(b[2].ptr, 16) && aligned(b[3].ptr, 16) &&
                      aligned(b[4].ptr, 8) && aligned(b[5].ptr, 8),
                  "bindings misaligned");
-    batch_rope_half_kernel<<<(uint32_t)((rows + 3) / 4), 256, 0, context_stream(c)>>>(
+    launch_timed(c, "batch_rope_half_kernel", batch_rope_half_kernel, dim3((uint32_t)((rows + 3) / 4)), dim3(256), 
         (const float *)b[0].ptr, (const float *)b[1].ptr, (const float *)b[2].ptr, (float *)b[3].ptr,
         (_Float16 *)b[4].ptr, (_Float16 *)b[5].ptr, (uint32_t)rows, p.pos, p.theta);
     return nullptr;

@@ -155,6 +155,16 @@ void *context_workspace(Context &c, uint64_t bytes) {
     return c.workspace;
 }
 
+void context_kernel_events(Context &c, const char *kernel, hipEvent_t *start, hipEvent_t *stop) {
+    *start = *stop = nullptr;
+    if (!c.wall_enabled || c.sample_mode != 3 || !c.active) return;
+    hipEvent_t a = next_event(&c), b = next_event(&c);
+    if (!a || !b) return;
+    *start = a;
+    *stop = b;
+    c.samples.push_back({kernel, a, b, -1});
+}
+
 // Ends the current sample of a multi-kernel dispatch and starts one named
 // `name` (used to time a split-K combine apart from its main kernel).
 void context_split(Context &c, const char *name) {
