@@ -142,6 +142,16 @@ struct DecodeParams {
 
 __device__ inline float sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+// x + x of lane l ^ 8 (the same position in the other half of its 16-lane row): one
+// DPP add. As inline assembly: the DPP move builtin was mis-scheduled here, and a
+// cross-lane shuffle costs an LDS round trip per value. The no-ops cover the wait
+// states before a DPP read of a VGPR just written and after.
+__device__ inline float add_row_partner(float x) {
+    float r;
+    asm volatile("s_nop 1\n\tv_add_f32_dpp %0, %1, %1 row_ror:8 row_mask:0xf bank_mask:0xf\n\ts_nop 1" : "=v"(r) : "v"(x));
+    return r;
+}
+
 // One chunk of one KV group in flight: thread t holds K rows t / 16 + 32 i (16 bytes
 // at 16 (t % 16)) and V page-row segments t / 8 + 64 i (16 bytes at 16 (t % 8)),
 // i < 4: every load instruction reads whole 256-byte K rows or whole 128-byte V
@@ -399,12 +409,12 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
     // ---- merge the eight waves: O^T[d][n] with d = 16*dt + 4*qq + r; heads sum hi + lo columns;
     // statistics are in base 2, O in units of vs_ref. The arena is free: the loop
     // ended with a barrier and no chunk is read again.
-    // the lo column n + 8 of each head joins its hi column n in registers (a lane
-    // swap inside each 16-lane row), then the hi lanes publish the head
+    // the lo column n + 8 of each head joins its hi column n in registers, then the
+    // hi lanes publish the head
 #pragma unroll
     for (int dt = 0; dt < 16; dt++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) o[dt][r] += __shfl_xor(o[dt][r], 8, 64);
+        for (int r = 0; r < 4; r++) o[dt][r] = add_row_partner(o[dt][r]);
     if (n < 8) {
 #pragma unroll
         for (int dt = 0; dt < 16; dt++)
