@@ -334,60 +334,60 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
 
     // one chunk from LDS: QK, the online softmax, PV
     auto compute = [&](const ChunkLds &b, uint32_t c) {
-            const int tl = 16 * wave + (lane & 15);          // the lane's K row of the chunk
-            // S^T: rows = tokens 16w + 4qq + r of the chunk, columns n
-            v4i acc = {0, 0, 0, 0};
-    #pragma unroll
-            for (int j = 0; j < 4; j++)
-                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, b.k[tl][(4 * j + qq) ^ (tl & 15)]), qi[j], acc, 0, 0, 0);
-            // the partner column n ^ 8 holds the other part of the same head
-            const int local0 = (int)(c * kChunk) + 16 * wave + 4 * qq;   // token offset inside the split
-            const uint32_t t0 = begin + (uint32_t)local0;
-            float sc[4];
-            float top = -INFINITY;
-    #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int mine = acc[r], other = __shfl_xor(mine, 8, 64);
-                const float full = ((float)(lo_col ? other : mine) + (float)(lo_col ? mine : other) * (1.0f / 254.0f)) * qsc;
-                const float value = t0 + r < end ? full * kscale[local0 + r] : -INFINITY;
-                sc[r] = value;
-                top = fmaxf(top, value);
-            }
-            top = fmaxf(top, __shfl_xor(top, 16, 64));
-            top = fmaxf(top, __shfl_xor(top, 32, 64));
-            const float next = fmaxf(m, top);
-            // a wave whose tokens are all past the split end keeps m = -inf: no decay
-            const float decay = next == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - next);
-            float total = 0.0f;
-            _Float16 hv[4];
-    #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const float prob = next == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc[r] - next);   // 0 for masked tokens
-                total += prob;
-                const float scaled = prob * (vscale[local0 + r] * vs_inv);
-                const _Float16 hi = (_Float16)scaled;
-                hv[r] = lo_col ? (_Float16)(scaled - (float)hi) : hi;
-            }
-            total += __shfl_xor(total, 16, 64);
-            total += __shfl_xor(total, 32, 64);
-            l = l * decay + total;
-            m = next;
-            if (decay != 1.0f) {
-    #pragma unroll
-                for (int i = 0; i < 16; i++) o[i] *= decay;
-            }
-            const half4 pop = {hv[0], hv[1], hv[2], hv[3]};
-            // V^T operand: row d = 16dt + n, the 4 codes of tokens 16w + 4qq + [0, 4)
-            const int vpiece = wave;   // tokens 16w..16w+15
-    #pragma unroll
-            for (int dt = 0; dt < 16; dt++) {
-                const int d = 16 * dt + n;
-                const uint32_t w4 = reinterpret_cast<const uint32_t *>(&b.v[d][vpiece ^ ((d >> 1) & 7)])[qq];
-                uint32_t h0, h1;
-                i8x4_to_f16(w4, h0, h1);
-                const half4 va = __builtin_bit_cast(half4, make_uint2(h0, h1));
-                o[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pop, o[dt], 0, 0, 0);
-            }
+        const int tl = 16 * wave + (lane & 15);          // the lane's K row of the chunk
+        // S^T: rows = tokens 16w + 4qq + r of the chunk, columns n
+        v4i acc = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, b.k[tl][(4 * j + qq) ^ (tl & 15)]), qi[j], acc, 0, 0, 0);
+        // the partner column n ^ 8 holds the other part of the same head
+        const int local0 = (int)(c * kChunk) + 16 * wave + 4 * qq;   // token offset inside the split
+        const uint32_t t0 = begin + (uint32_t)local0;
+        float sc[4];
+        float top = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int mine = acc[r], other = __shfl_xor(mine, 8, 64);
+            const float full = ((float)(lo_col ? other : mine) + (float)(lo_col ? mine : other) * (1.0f / 254.0f)) * qsc;
+            const float value = t0 + r < end ? full * kscale[local0 + r] : -INFINITY;
+            sc[r] = value;
+            top = fmaxf(top, value);
+        }
+        top = fmaxf(top, __shfl_xor(top, 16, 64));
+        top = fmaxf(top, __shfl_xor(top, 32, 64));
+        const float next = fmaxf(m, top);
+        // a wave whose tokens are all past the split end keeps m = -inf: no decay
+        const float decay = next == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - next);
+        float total = 0.0f;
+        _Float16 hv[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float prob = next == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc[r] - next);   // 0 for masked tokens
+            total += prob;
+            const float scaled = prob * (vscale[local0 + r] * vs_inv);
+            const _Float16 hi = (_Float16)scaled;
+            hv[r] = lo_col ? (_Float16)(scaled - (float)hi) : hi;
+        }
+        total += __shfl_xor(total, 16, 64);
+        total += __shfl_xor(total, 32, 64);
+        l = l * decay + total;
+        m = next;
+        if (decay != 1.0f) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) o[i] *= decay;
+        }
+        const half4 pop = {hv[0], hv[1], hv[2], hv[3]};
+        // V^T operand: row d = 16dt + n, the 4 codes of tokens 16w + 4qq + [0, 4)
+        const int vpiece = wave;   // tokens 16w..16w+15
+#pragma unroll
+        for (int dt = 0; dt < 16; dt++) {
+            const int d = 16 * dt + n;
+            const uint32_t w4 = reinterpret_cast<const uint32_t *>(&b.v[d][vpiece ^ ((d >> 1) & 7)])[qq];
+            uint32_t h0, h1;
+            i8x4_to_f16(w4, h0, h1);
+            const half4 va = __builtin_bit_cast(half4, make_uint2(h0, h1));
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pop, o[dt], 0, 0, 0);
+        }
     };
     // Chunks in pairs, so that the two register sets take turns without copies (a
     // copy of registers still being loaded waits for the load). At the top of a
@@ -410,7 +410,11 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
     // statistics are in base 2, O in units of vs_ref. The arena is free: the loop
     // ended with a barrier and no chunk is read again.
     // the lo column n + 8 of each head joins its hi column n in registers, then the
-    // hi lanes publish the head
+    // hi lanes publish the head. The DPP adds take MFMA results as inline-assembly
+    // operands, for which the compiler inserts no wait states: cover them here.
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int dt = 0; dt < 16; dt++)
 #pragma unroll
