@@ -20,8 +20,12 @@ namespace boot {
 namespace {
 
 constexpr int kTile = 16;               // tokens per store work-group (page-aligned tiles): 4 per wave
-constexpr int kVtStride = 20;           // bytes per LDS row of the V transpose (5 dwords: byte writes
-                                        // of a wave's 64 rows fall in 64 different banks)
+constexpr int kBulkTile = 64;           // tile of large appends: whole 64-byte V page-row runs
+constexpr uint64_t kBulkRows = 4096;    // appends of at least this many rows use kBulkTile
+// Bytes per LDS row of the V transpose: the tile plus 4, an odd number of dwords, so the
+// byte writes of a wave's 64 rows fall in 64 different banks.
+template <int Tile>
+constexpr int vt_stride() { return Tile + 4; }
 
 __device__ inline float wave_max(float v) {
 #pragma unroll
@@ -119,23 +123,25 @@ struct KNorm {
     float eps;
 };
 
-// Quantizes and appends tokens [lo, hi) of one 16-token tile for one KV head.
+// Quantizes and appends tokens [lo, hi) of one Tile-token tile for one KV head.
 // K: one wave per token, float4 per lane, codes written token-major as char4.
-// V: codes transposed in LDS, then written as page rows (16-byte stores for a
-// full tile, byte stores at partial tile edges), kernels.metal:126-128.
-template <bool Rope, bool Norm = false>
+// V: codes transposed in LDS, then written as page rows (Tile-byte runs for a full
+// tile, byte stores at partial tile edges), kernels.metal:126-128. Short runs cost
+// write bandwidth: 16-byte runs wrote 1.6x the bytes of a bulk append.
+template <bool Rope, bool Norm = false, int Tile = kTile>
 __device__ void store_tile(const float *__restrict__ k, const float *__restrict__ v,
                            int8_t *__restrict__ kc, int8_t *__restrict__ vc,
                            float *__restrict__ ks, float *__restrict__ vs,
                            uint32_t rows, uint32_t pos, uint32_t tile, uint32_t h,
                            uint8_t *vt, const float *inv_freq, KNorm knorm = {nullptr, 0.0f}) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t tile0 = tile * kTile;
-    const uint32_t lo = max(tile0, pos), hi = min(tile0 + kTile, pos + rows);
+    constexpr int kVtStride = vt_stride<Tile>();
+    const uint32_t tile0 = tile * Tile;
+    const uint32_t lo = max(tile0, pos), hi = min(tile0 + Tile, pos + rows);
     // Each wave takes tokens wave, wave+4, wave+8, wave+12 of the tile; their four
     // loads are issued before any is quantized so that the requests are in flight
     // together.
-    for (uint32_t tb = wave; tb < kTile; tb += 16) {
+    for (uint32_t tb = wave; tb < Tile; tb += 16) {
         float4 kx[4];
         float vx[4][4];
 #pragma unroll
@@ -173,11 +179,14 @@ __device__ void store_tile(const float *__restrict__ k, const float *__restrict_
     }
     __syncthreads();
     const uint64_t base = ((uint64_t)(tile0 >> 8) * 2 + h) * kPageBytes + (tile0 & 255);
-    if (lo == tile0 && hi == tile0 + kTile) {
-        // thread d writes the tile's 16 bytes of page row d
+    if (lo == tile0 && hi == tile0 + Tile) {
+        // thread d writes the tile's Tile bytes of page row d
         const int d = threadIdx.x;
         const uint32_t *src = reinterpret_cast<const uint32_t *>(vt + d * kVtStride);
-        *reinterpret_cast<uint4 *>(vc + base + (uint64_t)d * 256) = make_uint4(src[0], src[1], src[2], src[3]);
+#pragma unroll
+        for (int q = 0; q < Tile / 16; q++)
+            *reinterpret_cast<uint4 *>(vc + base + (uint64_t)d * 256 + 16 * q) =
+                make_uint4(src[4 * q], src[4 * q + 1], src[4 * q + 2], src[4 * q + 3]);
     } else {
         // partial tile (chunk edges, single-token decode appends): only the valid bytes
         const uint32_t count = hi - lo, first = lo - tile0;
@@ -188,13 +197,14 @@ __device__ void store_tile(const float *__restrict__ k, const float *__restrict_
     }
 }
 
+template <int Tile>
 __global__ __launch_bounds__(256) void kv_store_int8_kernel(
     const float *__restrict__ k, const float *__restrict__ v, int8_t *__restrict__ kc,
     int8_t *__restrict__ vc, float *__restrict__ ks, float *__restrict__ vs, uint32_t rows,
     uint32_t pos, uint32_t first_tile) {
-    __shared__ __attribute__((aligned(16))) uint8_t vt[256 * kVtStride];
-    store_tile<false>(k, v, kc, vc, ks, vs, rows, pos, first_tile + blockIdx.x / 2, blockIdx.x & 1,
-                      vt, nullptr);
+    __shared__ __attribute__((aligned(16))) uint8_t vt[256 * vt_stride<Tile>()];
+    store_tile<false, false, Tile>(k, v, kc, vc, ks, vs, rows, pos, first_tile + blockIdx.x / 2, blockIdx.x & 1,
+                                   vt, nullptr);
 }
 
 // batch_rope_int8 (kernels.metal:142-146): blocks [0, qblocks) rotate the
@@ -205,7 +215,7 @@ __global__ __launch_bounds__(256) void batch_rope_int8_kernel(
     float *__restrict__ qr, int8_t *__restrict__ kc, int8_t *__restrict__ vc,
     float *__restrict__ ks, float *__restrict__ vs, uint32_t rows, uint32_t pos, float theta,
     uint32_t qblocks, uint32_t first_tile) {
-    __shared__ __attribute__((aligned(16))) uint8_t vt[256 * kVtStride];
+    __shared__ __attribute__((aligned(16))) uint8_t vt[256 * vt_stride<kTile>()];
     __shared__ float inv_freq[32];
     fill_inv_freq(inv_freq, theta);
     __syncthreads();
@@ -239,7 +249,7 @@ __global__ __launch_bounds__(256) void prepare_fused_int8_kernel(
     float *__restrict__ gate, int8_t *__restrict__ kc, int8_t *__restrict__ vc, float *__restrict__ ks,
     float *__restrict__ vs, uint32_t rows, uint32_t pos, float theta, float eps, uint32_t qblocks,
     uint32_t first_tile) {
-    __shared__ __attribute__((aligned(16))) uint8_t vt[256 * kVtStride];
+    __shared__ __attribute__((aligned(16))) uint8_t vt[256 * vt_stride<kTile>()];
     __shared__ float inv_freq[32];
     fill_inv_freq(inv_freq, theta);
     __syncthreads();
@@ -379,11 +389,18 @@ const char *launch_kv_store_int8(Context &c, const View *b, int count, const boo
     BOOT_REQUIRE(b[0].bytes >= rows * 2048 && b[1].bytes >= rows * 2048, "K/V input smaller than rows*512 floats");
     BOOT_REQUIRE(aligned(b[0].ptr, 16) && aligned(b[1].ptr, 16), "K/V input bindings must be 16-byte aligned");
     if (const char *e = check_cache(b, 2, 3, 4, 5, end)) return e;
-    const uint32_t first = p.pos / kTile, last = (uint32_t)((end - 1) / kTile);
+    const bool bulk = rows >= kBulkRows;
+    const uint32_t tile = bulk ? kBulkTile : kTile;
+    const uint32_t first = p.pos / tile, last = (uint32_t)((end - 1) / tile);
     const uint32_t blocks = (last - first + 1) * 2;
-    launch_timed(c, "kv_store_int8_kernel", kv_store_int8_kernel, dim3(blocks), dim3(256), 
-        (const float *)b[0].ptr, (const float *)b[1].ptr, (int8_t *)b[2].ptr, (int8_t *)b[3].ptr,
-        (float *)b[4].ptr, (float *)b[5].ptr, (uint32_t)rows, p.pos, first);
+    if (bulk)
+        launch_timed(c, "kv_store_int8_kernel", kv_store_int8_kernel<kBulkTile>, dim3(blocks), dim3(256),
+                     (const float *)b[0].ptr, (const float *)b[1].ptr, (int8_t *)b[2].ptr, (int8_t *)b[3].ptr,
+                     (float *)b[4].ptr, (float *)b[5].ptr, (uint32_t)rows, p.pos, first);
+    else
+        launch_timed(c, "kv_store_int8_kernel", kv_store_int8_kernel<kTile>, dim3(blocks), dim3(256),
+                     (const float *)b[0].ptr, (const float *)b[1].ptr, (int8_t *)b[2].ptr, (int8_t *)b[3].ptr,
+                     (float *)b[4].ptr, (float *)b[5].ptr, (uint32_t)rows, p.pos, first);
     return nullptr;
 }
 

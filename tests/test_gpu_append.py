@@ -51,9 +51,10 @@ def test_config1_append_512_bitexact(device, oracle):
 
 
 @pytest.mark.parametrize("pos,rows", [(0, 1), (17, 7), (63, 2), (255, 2), (4093, 33), (1000, 600), (4096, 512),
-                                      (200000 - 37, 80)])
+                                      (200000 - 37, 80), (37, 5000), (8192, 8192), (65536 - 100, 4300)])
 def test_append_positions_and_guards(device, oracle, pos, rows):
-    """Unaligned starts, page crossings and single tokens; bytes outside the written range keep 0x55."""
+    """Unaligned starts, page crossings and single tokens; bytes outside the written range keep 0x55.
+    Appends of 4096 rows or more take the 64-token tiles (whole and partial ones)."""
     k, v = reference_kv(rows, seed=pos + rows)
     assert_same_bytes(*run_store(device, oracle, k, v, pos))
 
