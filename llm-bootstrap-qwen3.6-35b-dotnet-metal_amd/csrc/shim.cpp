@@ -92,9 +92,14 @@ hipEvent_t next_event(Context *c) {
     return c->events[c->events_used++];
 }
 
+// An event recorded on the context stream, or null when that fails (the sample it
+// belonged to is then dropped; timing never fails a command).
 hipEvent_t record(Context *c) {
     hipEvent_t e = next_event(c);
-    if (e) hipEventRecord(e, c->stream);
+    if (e && hipEventRecord(e, c->stream) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
     return e;
 }
 
@@ -140,7 +145,7 @@ void *context_workspace(Context &c, uint64_t bytes) {
     // Grow: the old scratch may still be read by enqueued work.
     if (hipStreamSynchronize(c.stream) != hipSuccess) return nullptr;
     if (c.workspace) {
-        hipFree(c.workspace);
+        if (hipFree(c.workspace) != hipSuccess) return nullptr;
         c.allocated -= c.workspace_bytes;
     }
     c.workspace = nullptr;
@@ -250,18 +255,19 @@ const char *boot_kernel_wall_json(void *handle) {
 void boot_destroy(void *handle) {
     Context *c = static_cast<Context *>(handle);
     if (!c) return;
-    hipStreamSynchronize(c->stream);
+    // teardown: an error here has no caller left to reach, so each call is best effort
+    (void)hipStreamSynchronize(c->stream);
     if (c->profile)
         for (auto &entry : c->timings)
             fprintf(stderr, "GPU_DIAGNOSTIC %s count=%llu gpu_ms=%.6f\n", entry.first.c_str(),
                     (unsigned long long)entry.second.second, entry.second.first * 1000);
     for (Buffer *b : c->buffers) {
-        hipFree(b->ptr);
+        (void)hipFree(b->ptr);
         delete b;
     }
-    if (c->workspace) hipFree(c->workspace);
-    for (hipEvent_t e : c->events) hipEventDestroy(e);
-    hipStreamDestroy(c->stream);
+    if (c->workspace) (void)hipFree(c->workspace);
+    for (hipEvent_t e : c->events) (void)hipEventDestroy(e);
+    (void)hipStreamDestroy(c->stream);
     delete c;
 }
 
@@ -270,12 +276,12 @@ void *boot_buffer(void *handle, uint64_t bytes) {
     if (bytes == 0) bytes = 4;
     void *p = nullptr;
     if (hipMalloc(&p, bytes) != hipSuccess) {
-        hipGetLastError();
+        (void)hipGetLastError();   // clear the error so the next call does not report it
         c->error = "HIP buffer allocation failed";
         return nullptr;
     }
     if (fill_zero(p, bytes, c->stream) != hipSuccess || hipStreamSynchronize(c->stream) != hipSuccess) {
-        hipFree(p);
+        (void)hipFree(p);   // the fill error is the one reported
         c->error = "HIP buffer zero fill failed";
         return nullptr;
     }
@@ -333,8 +339,10 @@ void boot_release_buffer(void *handle) {
     Buffer *b = static_cast<Buffer *>(handle);
     if (!b) return;
     Context *c = b->ctx;
-    hipStreamSynchronize(c->stream);  // enqueued work may still read it
-    hipFree(b->ptr);
+    // enqueued work may still read it; the call returns nothing, so failures land in
+    // the context's error text
+    if (hipStreamSynchronize(c->stream) != hipSuccess) c->error = "boot_release_buffer: stream synchronize failed";
+    if (hipFree(b->ptr) != hipSuccess) c->error = "boot_release_buffer: hipFree failed";
     c->allocated -= b->bytes;
     c->buffers.erase(b);
     delete b;
@@ -409,7 +417,7 @@ int boot_dispatch(void *handle, const char *name, void **buffers, const uint64_t
         hipEvent_t stop = record(c);
         if (!hip_ok(c, hipEventSynchronize(stop), name)) return 0;
         float ms = 0;
-        hipEventElapsedTime(&ms, serial_start, stop);
+        if (hipEventElapsedTime(&ms, serial_start, stop) != hipSuccess) ms = 0;
         auto &t = c->timings[name];
         t.first += ms * 1e-3;
         t.second++;
@@ -429,14 +437,16 @@ int boot_end(void *handle) {
     if (c->wall_enabled) {
         double done = wall_now();
         float ms = 0;
-        if (c->command_start && c->command_end) hipEventElapsedTime(&ms, c->command_start, c->command_end);
+        if (c->command_start && c->command_end && hipEventElapsedTime(&ms, c->command_start, c->command_end) != hipSuccess)
+            ms = 0;
         c->wall[0] += ms * 1e-3;
         c->wall[1] += before - c->begin_time;
         c->wall[3] += done - before;
         c->wall[4]++;
         for (auto &s : c->samples) {
             float sms = 0;
-            hipEventElapsedTime(&sms, s.start, s.end);
+            if (!s.start || !s.end) continue;   // an event that failed to record: no sample
+            if (hipEventElapsedTime(&sms, s.start, s.end) != hipSuccess) continue;
             auto &k = c->kernel_wall[s.name];
             k.first += sms * 1e-3;
             k.second++;
