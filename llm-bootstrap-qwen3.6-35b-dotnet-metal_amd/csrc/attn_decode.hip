@@ -469,10 +469,11 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
 }
 
 // Merges the splits of one (row, head) for 64 dimensions (grid: 4 dimension
-// chunks x 16 heads x rows). Two memory round trips: thread s first loads m_s
-// and l_s of every split at once (the block maximum, the weights
-// exp2(m_s - max) into LDS and the weighted sum of l), then 4 groups of 64 lanes
-// stream the float4 partials of every 4th split and the groups are added in LDS.
+// chunks x 16 heads x rows). Thread s loads m_s and l_s of every split at once (the
+// block maximum, the weights exp2(m_s - max) into LDS and the weighted sum of l);
+// 4 groups of 64 lanes take the float4 partials of every 4th split, the first 128
+// splits' partials loaded together with m and l since they do not depend on the
+// weights, and the groups are added in LDS.
 __global__ __launch_bounds__(256) void decode_combine_kernel(const float *__restrict__ partial, const float *__restrict__ gate,
                                                              float *__restrict__ y, uint32_t splits) {
     __shared__ float weight[kMaxDecodeSplits];
@@ -489,6 +490,22 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(const float *__rest
         ms[i] = tid + 256 * i < (int)splits ? base[(size_t)sidx * kPartialFloats + 2048 + h] : -INFINITY;
         ls[i] = base[(size_t)sidx * kPartialFloats + 2056 + h];
     }
+    // group `wave` takes splits wave, wave + 4, ...; lane: 4 dims of the 64-dim chunk,
+    // sub-lane `sub` the splits wave + 4 sub + 16 u
+    const uint32_t d = blockIdx.x * 64 + 4 * (lane & 15);
+    const int sub = lane >> 4;
+    const float *col = base + (size_t)h * 256 + d;
+    constexpr int kEarly = 8;
+    float4 pv[kEarly];
+#pragma unroll
+    for (int u = 0; u < kEarly; u++) {
+        const uint32_t sidx = min((uint32_t)(wave + 4 * sub + 16 * u), splits - 1);
+        pv[u] = *reinterpret_cast<const float4 *>(col + (size_t)sidx * kPartialFloats);
+    }
+    const size_t at = ((size_t)row * 16 + hq) * 256 + blockIdx.x * 64 + 4 * (tid & 15);
+    float gv[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) gv[i] = gate[at + i];   // y and gate need only 4-byte alignment
     float mmax = -INFINITY;
 #pragma unroll
     for (int i = 0; i < kPer; i++) mmax = fmaxf(mmax, ms[i]);
@@ -510,12 +527,17 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(const float *__rest
     if (lane == 0) lred[wave] = lsum;
     __syncthreads();
     lsum = (lred[0] + lred[1]) + (lred[2] + lred[3]);
-    // group `wave` takes splits wave, wave + 4, ...; lane: 4 dims of the 64-dim chunk
-    const uint32_t d = blockIdx.x * 64 + 4 * (lane & 15);
-    const int sub = lane >> 4;   // 4 sub-lanes per dim quad: splits wave + 4 (4j + sub)
-    const float *col = base + (size_t)h * 256 + d;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (uint32_t s0 = wave + 4 * sub; s0 < splits; s0 += 64) {
+#pragma unroll
+    for (int u = 0; u < kEarly; u++) {
+        const uint32_t sidx = wave + 4 * sub + 16 * u;
+        const float w = sidx < splits ? weight[sidx] : 0.0f;
+        acc.x += pv[u].x * w;
+        acc.y += pv[u].y * w;
+        acc.z += pv[u].z * w;
+        acc.w += pv[u].w * w;
+    }
+    for (uint32_t s0 = wave + 4 * sub + 16 * kEarly; s0 < splits; s0 += 64) {
         float4 v[4];
         float w[4];
 #pragma unroll
@@ -552,12 +574,11 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(const float *__rest
             t.z += sums[w][tid].z;
             t.w += sums[w][tid].w;
         }
-        const size_t at = ((size_t)row * 16 + hq) * 256 + blockIdx.x * 64 + 4 * tid;
         const float inv = 1.0f / lsum;
-        y[at + 0] = t.x * inv * sigmoidf(gate[at + 0]);   // y and gate need only 4-byte alignment
-        y[at + 1] = t.y * inv * sigmoidf(gate[at + 1]);
-        y[at + 2] = t.z * inv * sigmoidf(gate[at + 2]);
-        y[at + 3] = t.w * inv * sigmoidf(gate[at + 3]);
+        y[at + 0] = t.x * inv * sigmoidf(gv[0]);
+        y[at + 1] = t.y * inv * sigmoidf(gv[1]);
+        y[at + 2] = t.z * inv * sigmoidf(gv[2]);
+        y[at + 3] = t.w * inv * sigmoidf(gv[3]);
     }
 }
 

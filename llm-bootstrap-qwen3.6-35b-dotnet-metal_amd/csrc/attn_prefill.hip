@@ -702,8 +702,9 @@ __global__ __launch_bounds__(512, 1) void prefill_pp_kernel(PrefillParams p) {
 }
 
 // Merges the split partials (O^T scaled by vs_ref, m, l in base 2): one wave per
-// logical row, four dimensions per lane; the maxima of all splits first, then the
-// partials eight splits at a time so their loads are in flight together.
+// logical row, four dimensions per lane, eight splits per step with all their loads
+// in flight together and a running maximum across steps, so a chunk with at most
+// eight splits makes one memory round trip.
 template <int kTileRows>
 __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillParams p) {
     constexpr size_t kStride = (size_t)kTileRows * 256 + 2 * kTileRows;
@@ -712,12 +713,11 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillParams p) {
     const uint32_t row = tile * kTileRows + local_row;
     if (row >= p.rows * 8) return;   // wave-uniform
     const float *base = p.partial + ((size_t)g * p.tiles + tile) * p.splits * kStride;
-    float mmax = -INFINITY;
-    for (uint32_t s = lane; s < p.splits; s += 64) mmax = fmaxf(mmax, base[s * kStride + (size_t)kTileRows * 256 + local_row]);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, o, 64));
+    const uint32_t token = row / 8, head = g * 8 + row % 8;
+    const size_t at = ((size_t)token * 16 + head) * 256 + 4 * lane;
+    const float4 gv = *reinterpret_cast<const float4 *>(p.gate + at);
+    float mrun = -INFINITY, lsum = 0.0f;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    float lsum = 0.0f;
     for (uint32_t s0 = 0; s0 < p.splits; s0 += 8) {
         float ms[8], ls[8];
         float4 os[8];
@@ -729,10 +729,22 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillParams p) {
             ls[j] = part[(size_t)kTileRows * 256 + kTileRows + local_row];
             os[j] = *reinterpret_cast<const float4 *>(part + (size_t)local_row * 256 + 4 * lane);
         }
+        float mstep = ms[0];
+#pragma unroll
+        for (int j = 1; j < 8; j++) mstep = fmaxf(mstep, ms[j]);
+        if (mstep == -INFINITY) continue;   // wave-uniform: every split of the step is empty
+        const float mnew = fmaxf(mrun, mstep);
+        const float decay = mrun == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mrun - mnew);
+        mrun = mnew;
+        lsum *= decay;
+        acc.x *= decay;
+        acc.y *= decay;
+        acc.z *= decay;
+        acc.w *= decay;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             if (ms[j] == -INFINITY) continue;
-            const float f = __builtin_amdgcn_exp2f(ms[j] - mmax);
+            const float f = __builtin_amdgcn_exp2f(ms[j] - mnew);
             lsum += ls[j] * f;
             acc.x += os[j].x * f;
             acc.y += os[j].y * f;
@@ -740,9 +752,6 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillParams p) {
             acc.w += os[j].w * f;
         }
     }
-    const uint32_t token = row / 8, head = g * 8 + row % 8;
-    const size_t at = ((size_t)token * 16 + head) * 256 + 4 * lane;
-    const float4 gv = *reinterpret_cast<const float4 *>(p.gate + at);
     const float inv = 1.0f / lsum;
     float4 out;
     out.x = acc.x * inv * sigmoidf(gv.x);
