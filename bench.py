@@ -296,10 +296,10 @@ def main():
     device.reset_wall_timing(kernels_exact=True)
     for _ in range(args.steps):
         work.step()
-    ks = kernel_stats(device, ["prefill_pp_kernel", "prefill_combine_kernel<256>", "batch_rope_int8_kernel",
+    ks = kernel_stats(device, ["prefill_pp_kernel", "prefill_combine_half_kernel", "batch_rope_int8_kernel",
                                "query_grouped_half_kernel"])
     attn_ms = ks["prefill_pp_kernel"][0] / args.steps
-    combine_ms = ks.get("prefill_combine_kernel<256>", (0.0, 0))[0] / args.steps
+    combine_ms = ks.get("prefill_combine_half_kernel", (0.0, 0))[0] / args.steps
     launches = ks["prefill_pp_kernel"][1] // args.steps
     flops = work.flops()
     achieved = flops / (attn_ms * 1e-3) / 1e12

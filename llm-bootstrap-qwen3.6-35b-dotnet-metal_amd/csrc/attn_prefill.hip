@@ -341,7 +341,9 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillParams p) {
 constexpr int kPPRows = 256;               // logical rows per work-group
 constexpr int kPPKeys = 32;                // keys per tile
 constexpr int kPPVStride = kPPKeys + 8;    // FP16 V^T tile row stride (halves): 80 bytes
-constexpr size_t kPPPartialStride = (size_t)kPPRows * 256 + 2 * kPPRows;
+// Split partial of one work-group: O^T / l per row as FP16 (|value| <= 127: a mean of V
+// codes weighted by V scale / vs_ref <= 1), then m, l and vs_ref per row as floats.
+constexpr size_t kPPPartialBytes = (size_t)kPPRows * 256 * 2 + 3 * kPPRows * 4;
 constexpr int kPPQRegs = 6;                // Q^T operand chunks held in registers; the rest in LDS
 
 // Max over the lane pair (l, l ^ 32). v_permlane32_swap exchanges lanes 32-63 of
@@ -684,20 +686,26 @@ __global__ __launch_bounds__(512, 1) void prefill_pp_kernel(PrefillParams p) {
             }
         return;
     }
-    float *part = p.partial + (((size_t)g * p.tiles + tile) * p.splits + split) * kPPPartialStride;
+    unsigned char *pbase = reinterpret_cast<unsigned char *>(p.partial) +
+                           (((size_t)g * p.tiles + tile) * p.splits + split) * kPPPartialBytes;
     const int local_row = 32 * wave + i;
+    const float inv_l = l > 0.0f ? 1.0f / l : 0.0f;
+    typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+    _Float16 *po = reinterpret_cast<_Float16 *>(pbase) + (size_t)local_row * 256;
 #pragma unroll
     for (int dt = 0; dt < 8; dt++)
 #pragma unroll
         for (int vq = 0; vq < 4; vq++) {
             const int d = 32 * dt + 8 * vq + 4 * kk;
-            *reinterpret_cast<float4 *>(part + (size_t)local_row * 256 + d) =
-                make_float4(o[dt][4 * vq] * vs_ref, o[dt][4 * vq + 1] * vs_ref, o[dt][4 * vq + 2] * vs_ref,
-                            o[dt][4 * vq + 3] * vs_ref);
+            const half4 hv = {(_Float16)(o[dt][4 * vq] * inv_l), (_Float16)(o[dt][4 * vq + 1] * inv_l),
+                              (_Float16)(o[dt][4 * vq + 2] * inv_l), (_Float16)(o[dt][4 * vq + 3] * inv_l)};
+            *reinterpret_cast<half4 *>(po + d) = hv;
         }
     if (kk == 0) {
-        part[(size_t)kPPRows * 256 + local_row] = m;
-        part[(size_t)kPPRows * 256 + kPPRows + local_row] = l;
+        float *stat = reinterpret_cast<float *>(pbase + (size_t)kPPRows * 256 * 2);
+        stat[local_row] = m;
+        stat[kPPRows + local_row] = l;
+        stat[2 * kPPRows + local_row] = vs_ref;
     }
 }
 
@@ -761,6 +769,69 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillParams p) {
     *reinterpret_cast<float4 *>(p.y + at) = out;
 }
 
+// Merges the FP16 split partials of prefill_pp_kernel (O^T / l, then m, l, vs_ref per
+// row): one wave per logical row, four dimensions per lane, eight splits per step with
+// a running maximum, as prefill_combine_kernel.
+__global__ __launch_bounds__(256) void prefill_combine_half_kernel(PrefillParams p) {
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t local_row = blockIdx.x * 4 + (threadIdx.x >> 6), tile = blockIdx.y, g = blockIdx.z;
+    const uint32_t row = tile * kPPRows + local_row;
+    if (row >= p.rows * 8) return;   // wave-uniform
+    const unsigned char *base = reinterpret_cast<const unsigned char *>(p.partial) +
+                                ((size_t)g * p.tiles + tile) * p.splits * kPPPartialBytes;
+    const uint32_t token = row / 8, head = g * 8 + row % 8;
+    const size_t at = ((size_t)token * 16 + head) * 256 + 4 * lane;
+    const float4 gv = *reinterpret_cast<const float4 *>(p.gate + at);
+    typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+    float mrun = -INFINITY, lsum = 0.0f;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (uint32_t s0 = 0; s0 < p.splits; s0 += 8) {
+        float ms[8], ls[8], ws[8];
+        half4 os[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t s = min(s0 + j, p.splits - 1);
+            const unsigned char *part = base + s * kPPPartialBytes;
+            const float *stat = reinterpret_cast<const float *>(part + (size_t)kPPRows * 256 * 2);
+            ms[j] = s0 + j < p.splits ? stat[local_row] : -INFINITY;
+            ls[j] = stat[kPPRows + local_row];
+            ws[j] = stat[2 * kPPRows + local_row];
+            os[j] = *reinterpret_cast<const half4 *>(reinterpret_cast<const _Float16 *>(part) + (size_t)local_row * 256 + 4 * lane);
+        }
+        float mstep = ms[0];
+#pragma unroll
+        for (int j = 1; j < 8; j++) mstep = fmaxf(mstep, ms[j]);
+        if (mstep == -INFINITY) continue;   // wave-uniform: every split of the step is empty
+        const float mnew = fmaxf(mrun, mstep);
+        const float decay = mrun == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mrun - mnew);
+        mrun = mnew;
+        lsum *= decay;
+        acc.x *= decay;
+        acc.y *= decay;
+        acc.z *= decay;
+        acc.w *= decay;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            if (ms[j] == -INFINITY) continue;
+            const float f = __builtin_amdgcn_exp2f(ms[j] - mnew);
+            const float lf = ls[j] * f;
+            const float wf = lf * ws[j];
+            lsum += lf;
+            acc.x += (float)os[j].x * wf;
+            acc.y += (float)os[j].y * wf;
+            acc.z += (float)os[j].z * wf;
+            acc.w += (float)os[j].w * wf;
+        }
+    }
+    const float inv = 1.0f / lsum;
+    float4 out;
+    out.x = acc.x * inv * sigmoidf(gv.x);
+    out.y = acc.y * inv * sigmoidf(gv.y);
+    out.z = acc.z * inv * sigmoidf(gv.z);
+    out.w = acc.w * inv * sigmoidf(gv.w);
+    *reinterpret_cast<float4 *>(p.y + at) = out;
+}
+
 inline bool aligned(const void *ptr, uintptr_t a) { return (reinterpret_cast<uintptr_t>(ptr) & (a - 1)) == 0; }
 
 }  // namespace
@@ -803,7 +874,7 @@ const char *launch_prefill(Context &c, const View *b, int count, const boot_kern
     const uint64_t tile_rows = int8 ? kPPRows : kRows;
     const uint64_t tile_keys = int8 ? kPPKeys : kKeys;
     const uint64_t per_cu = int8 ? 1 : 2;
-    const size_t stride = int8 ? kPPPartialStride : kPartialStride;
+    const size_t stride_bytes = int8 ? kPPPartialBytes : kPartialStride * sizeof(float);
     p.tiles = (uint32_t)((rows * 8 + tile_rows - 1) / tile_rows);
     // split-K: enough blocks to fill the CUs, each split at least 256 keys
     const uint64_t base_blocks = 2ull * p.tiles;
@@ -819,7 +890,7 @@ const char *launch_prefill(Context &c, const View *b, int count, const boot_kern
     p.remap = ((2 * splits) % 8 == 0) ? 1u : 0u;
     p.partial = nullptr;
     if (splits > 1) {
-        p.partial = (float *)context_workspace(c, base_blocks * splits * stride * sizeof(float));
+        p.partial = (float *)context_workspace(c, base_blocks * splits * stride_bytes);
         BOOT_REQUIRE(p.partial, "cannot allocate prefill split workspace");
     }
     if (int8)
@@ -829,7 +900,7 @@ const char *launch_prefill(Context &c, const View *b, int count, const boot_kern
     if (splits > 1) {
         context_split(c, int8 ? "attention_online_int8.combine" : "attention_online_fp16.combine");
         if (int8)
-            launch_timed(c, "prefill_combine_kernel<256>", prefill_combine_kernel<kPPRows>, dim3(kPPRows / 4, p.tiles, 2), dim3(256), p);
+            launch_timed(c, "prefill_combine_half_kernel", prefill_combine_half_kernel, dim3(kPPRows / 4, p.tiles, 2), dim3(256), p);
         else
             launch_timed(c, "prefill_combine_kernel<128>", prefill_combine_kernel<kRows>, dim3(kRows / 4, p.tiles, 2), dim3(256), p);
     }
