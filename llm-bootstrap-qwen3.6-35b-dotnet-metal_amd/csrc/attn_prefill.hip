@@ -410,32 +410,7 @@ __global__ __launch_bounds__(512, 1) void prefill_pp_kernel(PrefillParams p) {
     const int ntiles = kend > kbeg ? (int)((kend - kbeg + kPPKeys - 1) / kPPKeys) : 0;
     const uint32_t wave_min_limit = p.pos + min(R - 1, r0 + 32 * wave) / 8;
 
-    // Q^T operands (B of the QK product): lane (i, kk), dims 16c + 8kk + [0, 8); the
-    // last chunks wait in LDS, each lane reading back only what it wrote
-    half8 qop[kPPQRegs];
-    {
-        const _Float16 *qrow = p.q + ((size_t)g * R + rr) * 256 + 8 * kk;
-#pragma unroll
-        for (int c = 0; c < kPPQRegs; c++) qop[c] = *reinterpret_cast<const half8 *>(qrow + 16 * c);
-#pragma unroll
-        for (int c = kPPQRegs; c < 16; c++) qlds[c - kPPQRegs][tid] = *reinterpret_cast<const uint4 *>(qrow + 16 * c);
-    }
-
-    // vs_ref: the largest V scale over this block's keys (0 if all are 0)
-    float vs_ref = 0.0f;
-    for (uint32_t key = kbeg + tid; key < kend; key += 512) vs_ref = fmaxf(vs_ref, p.vs[(size_t)key * 2 + g]);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) vs_ref = fmaxf(vs_ref, __shfl_xor(vs_ref, o, 64));
-    if (lane == 0) vs_partial[wave] = vs_ref;
-    __syncthreads();
-    vs_ref = vs_partial[0];
-#pragma unroll
-    for (int w = 1; w < 8; w++) vs_ref = fmaxf(vs_ref, vs_partial[w]);
-    // work-group uniform: scalar registers
-    vs_ref = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, vs_ref)));
-    const float vs_inv = __builtin_bit_cast(
-        float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, vs_ref > 0.0f ? 1.0f / vs_ref : 0.0f)));
-
+    float vs_ref = 0.0f, vs_inv = 0.0f;   // set once the prologue's loads are in (below)
     // Staging of the FP16 tiles. Team 0 thread t (wave t / 64 of the team, lane t % 64): K rows
     // 8 (t / 64) + 4j + (t % 64) / 16 for j = 0, 1, 16 codes at 16 (t % 16); a load
     // instruction reads four whole 256-byte rows. Team 1 thread t: dimension t of
@@ -490,9 +465,46 @@ __global__ __launch_bounds__(512, 1) void prefill_pp_kernel(PrefillParams p) {
         return h;
     };
 
+    // The prologue's loads go out together (one memory round trip): the V scales of
+    // the block's first 4096 keys (vs_ref), the codes and scales of tile 0, the query.
+    float vsv[8];
+#pragma unroll
+    for (int it = 0; it < 8; it++) {
+        const uint32_t key = kbeg + tid + 512 * it;
+        vsv[it] = key < kend ? p.vs[(size_t)key * 2 + g] : 0.0f;
+    }
     if (ntiles > 0) {
         load_raw(kbeg);
         load_scales(kbeg);
+    }
+    // Q^T operands (B of the QK product): lane (i, kk), dims 16c + 8kk + [0, 8); the
+    // last chunks wait in LDS, each lane reading back only what it wrote
+    half8 qop[kPPQRegs];
+    {
+        const _Float16 *qrow = p.q + ((size_t)g * R + rr) * 256 + 8 * kk;
+#pragma unroll
+        for (int c = 0; c < kPPQRegs; c++) qop[c] = *reinterpret_cast<const half8 *>(qrow + 16 * c);
+#pragma unroll
+        for (int c = kPPQRegs; c < 16; c++) qlds[c - kPPQRegs][tid] = *reinterpret_cast<const uint4 *>(qrow + 16 * c);
+    }
+
+    // vs_ref: the largest V scale over this block's keys (0 if all are 0)
+#pragma unroll
+    for (int it = 0; it < 8; it++) vs_ref = fmaxf(vs_ref, vsv[it]);
+    for (uint32_t key = kbeg + tid + 4096; key < kend; key += 512) vs_ref = fmaxf(vs_ref, p.vs[(size_t)key * 2 + g]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) vs_ref = fmaxf(vs_ref, __shfl_xor(vs_ref, o, 64));
+    if (lane == 0) vs_partial[wave] = vs_ref;
+    __syncthreads();
+    vs_ref = vs_partial[0];
+#pragma unroll
+    for (int w = 1; w < 8; w++) vs_ref = fmaxf(vs_ref, vs_partial[w]);
+    // work-group uniform: scalar registers
+    vs_ref = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, vs_ref)));
+    vs_inv = __builtin_bit_cast(
+        float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, vs_ref > 0.0f ? 1.0f / vs_ref : 0.0f)));
+
+    if (ntiles > 0) {
 #pragma unroll
         for (int q = 0; q < 4; q++) *quad_dst(buf[0], q) = convert_quad(q);
         store_scales(buf[0], kbeg);
