@@ -142,14 +142,29 @@ struct DecodeParams {
 
 __device__ inline float sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-// x + x of lane l ^ 8 (the same position in the other half of its 16-lane row): one
-// DPP add. As inline assembly: the DPP move builtin was mis-scheduled here, and a
-// cross-lane shuffle costs an LDS round trip per value. The no-ops cover the wait
-// states before a DPP read of a VGPR just written and after.
-__device__ inline float add_row_partner(float x) {
-    float r;
-    asm volatile("s_nop 1\n\tv_add_f32_dpp %0, %1, %1 row_ror:8 row_mask:0xf bank_mask:0xf\n\ts_nop 1" : "=v"(r) : "v"(x));
-    return r;
+// x + x of lane l ^ 8 (the same position in the other half of its 16-lane row) for
+// the eight values of two accumulators: one DPP add each, as inline assembly (the DPP
+// move builtin was mis-scheduled here, and a cross-lane shuffle costs an LDS round
+// trip per value). The sources are MFMA results whose wait states the caller has
+// covered and no add reads another's result, so only the block's ends need wait
+// states (a register copy the compiler places just before the block).
+__device__ inline void add_row_partner8(floatx4 &a, floatx4 &b) {
+    float r0, r1, r2, r3, r4, r5, r6, r7;
+    asm volatile(
+        "s_nop 1\n\t"
+        "v_add_f32_dpp %0, %8, %8 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32_dpp %1, %9, %9 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32_dpp %2, %10, %10 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32_dpp %3, %11, %11 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32_dpp %4, %12, %12 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32_dpp %5, %13, %13 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32_dpp %6, %14, %14 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_add_f32_dpp %7, %15, %15 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 1"
+        : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3), "=&v"(r4), "=&v"(r5), "=&v"(r6), "=&v"(r7)
+        : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(b[0]), "v"(b[1]), "v"(b[2]), "v"(b[3]));
+    a = floatx4{r0, r1, r2, r3};
+    b = floatx4{r4, r5, r6, r7};
 }
 
 // One chunk of one KV group in flight: thread t holds K rows t / 16 + 32 i (16 bytes
@@ -391,24 +406,47 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
     };
     // Chunks in pairs, so that the two register sets take turns without copies (a
     // copy of registers still being loaded waits for the load). At the top of a
-    // pair: buffer 0 holds chunk c, r1 chunk c + 1, r2 chunk c + 2. The odd tail only
-    // skips a compute; the loads and barriers stay unconditional. (A third register
+    // pair: buffer 0 holds chunk c, r1 chunk c + 1, r2 chunk c + 2. The pairs run
+    // while every load is a real chunk (a fixed count per pair keeps the counter
+    // waits exact); the last one to four chunks follow without loads past the end,
+    // whose registers the merge below would otherwise wait for. (A third register
     // set, three chunks in flight, measured slower: the longer start-up burst delays
     // every work-group's first chunk.)
-    for (uint32_t c = 0; c < nchunks; c += 2) {
+    uint32_t c = 0;
+    for (; c + 4 < nchunks; c += 2) {
         compute(bufs[0], c);
         store_chunk(bufs[1], r1, tid);   // buffer 1's chunk c - 1 was finished before the last barrier
         load_chunk(r1, p, g, begin, c + 3, nchunks, length, tid);
         __syncthreads();
-        if (c + 1 < nchunks) compute(bufs[1], c + 1);
+        compute(bufs[1], c + 1);
         store_chunk(bufs[0], r2, tid);
         load_chunk(r2, p, g, begin, c + 4, nchunks, length, tid);
         __syncthreads();
     }
+    if (c < nchunks) {
+        compute(bufs[0], c);
+        if (c + 1 < nchunks) {
+            store_chunk(bufs[1], r1, tid);
+            if (c + 3 < nchunks) load_chunk(r1, p, g, begin, c + 3, nchunks, length, tid);
+            __syncthreads();
+            compute(bufs[1], c + 1);
+            if (c + 2 < nchunks) {
+                store_chunk(bufs[0], r2, tid);
+                __syncthreads();
+                compute(bufs[0], c + 2);
+                if (c + 3 < nchunks) {
+                    store_chunk(bufs[1], r1, tid);
+                    __syncthreads();
+                    compute(bufs[1], c + 3);
+                }
+            }
+        }
+    }
+    __syncthreads();
 
     // ---- merge the eight waves: O^T[d][n] with d = 16*dt + 4*qq + r; heads sum hi + lo columns;
-    // statistics are in base 2, O in units of vs_ref. The arena is free: the loop
-    // ended with a barrier and no chunk is read again.
+    // statistics are in base 2, O in units of vs_ref. The arena is free: the chunks
+    // ended with a barrier and none is read again.
     // the lo column n + 8 of each head joins its hi column n in registers, then the
     // hi lanes publish the head. The DPP adds take MFMA results as inline-assembly
     // operands, for which the compiler inserts no wait states: cover them here.
@@ -416,14 +454,16 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int dt = 0; dt < 16; dt++)
+    for (int dt = 0; dt < 16; dt += 2) add_row_partner8(o[dt], o[dt + 1]);
+    {
+        // lanes n and n + 8 now hold the same sums: each half of the row writes half of them
+        const bool upper = n >= 8;
 #pragma unroll
-        for (int r = 0; r < 4; r++) o[dt][r] = add_row_partner(o[dt][r]);
-    if (n < 8) {
-#pragma unroll
-        for (int dt = 0; dt < 16; dt++)
-            *reinterpret_cast<floatx4 *>(&merge_o[wave][head][16 * dt + 4 * qq]) = o[dt];
-        if (qq == 0) {
+        for (int j = 0; j < 8; j++) {
+            const floatx4 val = upper ? o[8 + j] : o[j];
+            *reinterpret_cast<floatx4 *>(&merge_o[wave][head][16 * (j + (upper ? 8 : 0)) + 4 * qq]) = val;
+        }
+        if (n < 8 && qq == 0) {
             merge_m[wave][head] = m;
             merge_l[wave][head] = l;
         }
