@@ -47,15 +47,16 @@ __device__ inline uint32_t pack4(float a, float b, float c, float d) {
 // Rotation angles of one position for the four dims a lane holds (4*lane .. +3):
 // lane j < 32 evaluates cos/sin of position * theta^(-2j/64) once
 // (kernels.metal:122-125), and lanes fetch the pairs of their dims
-// (j = d % 32) by shuffle, so one sincos per pair serves every head.
+// (j = d % 32) by shuffle, so one sincos per pair serves every head. `ifreq` is
+// the lane's theta^(-2j/64) from lane_inv_freq.
 struct Rope4 {
     float c[4], s[4];
 };
 
-__device__ inline Rope4 rope_angles(uint32_t position, int lane, const float *inv_freq) {
+__device__ inline Rope4 rope_angles(uint32_t position, int lane, float ifreq) {
     float cj = 1.0f, sj = 0.0f;
     if (lane < 32) {
-        const float angle = (float)position * inv_freq[lane];
+        const float angle = (float)position * ifreq;
         sincosf(angle, &sj, &cj);
     }
     Rope4 r;
@@ -88,9 +89,11 @@ __device__ inline float4 rope4(float4 x, int lane, const Rope4 &r) {
     return make_float4(out[0], out[1], out[2], out[3]);
 }
 
-__device__ inline void fill_inv_freq(float *inv_freq, float theta) {
-    // pow(theta, -float(2*j)/64.0f) in fp32, kernels.metal:123
-    if (threadIdx.x < 32) inv_freq[threadIdx.x] = powf(theta, -(float)(2 * threadIdx.x) / 64.0f);
+// pow(theta, -float(2*j)/64.0f) in fp32 for lane j < 32 (kernels.metal:123), computed
+// per wave in registers: no LDS table and no barrier, so a kernel's loads go out first.
+__device__ inline float lane_inv_freq(float theta) {
+    const int j = threadIdx.x & 63;
+    return j < 32 ? powf(theta, -(float)(2 * j) / 64.0f) : 0.0f;
 }
 
 // RMS normalization of one 256-dim vector held as a float4 per lane, with the
@@ -133,7 +136,7 @@ __device__ void store_tile(const float *__restrict__ k, const float *__restrict_
                            int8_t *__restrict__ kc, int8_t *__restrict__ vc,
                            float *__restrict__ ks, float *__restrict__ vs,
                            uint32_t rows, uint32_t pos, uint32_t tile, uint32_t h,
-                           uint8_t *vt, const float *inv_freq, KNorm knorm = {nullptr, 0.0f}) {
+                           uint8_t *vt, float ifreq, KNorm knorm = {nullptr, 0.0f}) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     constexpr int kVtStride = vt_stride<Tile>();
     const uint32_t tile0 = tile * Tile;
@@ -160,7 +163,7 @@ __device__ void store_tile(const float *__restrict__ k, const float *__restrict_
             if (t < lo || t >= hi) continue;  // wave-uniform
             float4 kv = kx[u];
             if (Norm) kv = rms_norm4(kv, knorm.eps, knorm.w, lane, 1.0f);
-            if (Rope) kv = rope4(kv, lane, rope_angles(t, lane, inv_freq));
+            if (Rope) kv = rope4(kv, lane, rope_angles(t, lane, ifreq));
             const float ka = wave_max(fmaxf(fmaxf(fabsf(kv.x), fabsf(kv.y)), fmaxf(fabsf(kv.z), fabsf(kv.w))));
             const float va = wave_max(fmaxf(fmaxf(fabsf(vx[u][0]), fabsf(vx[u][1])), fmaxf(fabsf(vx[u][2]), fabsf(vx[u][3]))));
             const uint64_t vector = (uint64_t)t * 2 + h;
@@ -204,7 +207,7 @@ __global__ __launch_bounds__(256) void kv_store_int8_kernel(
     uint32_t pos, uint32_t first_tile) {
     __shared__ __attribute__((aligned(16))) uint8_t vt[256 * vt_stride<Tile>()];
     store_tile<false, false, Tile>(k, v, kc, vc, ks, vs, rows, pos, first_tile + blockIdx.x / 2, blockIdx.x & 1,
-                                   vt, nullptr);
+                                   vt, 0.0f);
 }
 
 // batch_rope_int8 (kernels.metal:142-146): blocks [0, qblocks) rotate the
@@ -216,15 +219,13 @@ __global__ __launch_bounds__(256) void batch_rope_int8_kernel(
     float *__restrict__ ks, float *__restrict__ vs, uint32_t rows, uint32_t pos, float theta,
     uint32_t qblocks, uint32_t first_tile) {
     __shared__ __attribute__((aligned(16))) uint8_t vt[256 * vt_stride<kTile>()];
-    __shared__ float inv_freq[32];
-    fill_inv_freq(inv_freq, theta);
-    __syncthreads();
+    const float ifreq = lane_inv_freq(theta);
     if (blockIdx.x < qblocks) {
         // one wave per row: the angles are computed once and reused by its 16 heads
         const int lane = threadIdx.x & 63;
         const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
         if (row >= rows) return;                                     // wave-uniform
-        const Rope4 r = rope_angles(pos + row, lane, inv_freq);
+        const Rope4 r = rope_angles(pos + row, lane, ifreq);
         const float *src = q + (size_t)row * 4096 + 4 * lane;
         float *dst = qr + (size_t)row * 4096 + 4 * lane;
         float4 x[16];
@@ -235,7 +236,7 @@ __global__ __launch_bounds__(256) void batch_rope_int8_kernel(
         return;
     }
     const uint32_t b = blockIdx.x - qblocks;
-    store_tile<true>(k, v, kc, vc, ks, vs, rows, pos, first_tile + b / 2, b & 1, vt, inv_freq);
+    store_tile<true>(k, v, kc, vc, ks, vs, rows, pos, first_tile + b / 2, b & 1, vt, ifreq);
 }
 
 // attention_prepare_fused_int8 (kernels.metal:1902-1914): per row, the 16
@@ -250,14 +251,12 @@ __global__ __launch_bounds__(256) void prepare_fused_int8_kernel(
     float *__restrict__ vs, uint32_t rows, uint32_t pos, float theta, float eps, uint32_t qblocks,
     uint32_t first_tile) {
     __shared__ __attribute__((aligned(16))) uint8_t vt[256 * vt_stride<kTile>()];
-    __shared__ float inv_freq[32];
-    fill_inv_freq(inv_freq, theta);
-    __syncthreads();
+    const float ifreq = lane_inv_freq(theta);
     if (blockIdx.x < qblocks) {
         const int lane = threadIdx.x & 63;
         const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
         if (row >= rows) return;                                     // wave-uniform
-        const Rope4 r = rope_angles(pos + row, lane, inv_freq);
+        const Rope4 r = rope_angles(pos + row, lane, ifreq);
         typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 #pragma unroll 4
         for (int h = 0; h < 16; h++) {
@@ -272,7 +271,7 @@ __global__ __launch_bounds__(256) void prepare_fused_int8_kernel(
         return;
     }
     const uint32_t b = blockIdx.x - qblocks;
-    store_tile<true, true>(k, v, kc, vc, ks, vs, rows, pos, first_tile + b / 2, b & 1, vt, inv_freq, KNorm{kw, eps});
+    store_tile<true, true>(k, v, kc, vc, ks, vs, rows, pos, first_tile + b / 2, b & 1, vt, ifreq, KNorm{kw, eps});
 }
 
 // batch_rope with FP16 KV storage (flags bit 256; kernels.metal:16-21, 322-324):
@@ -282,13 +281,11 @@ __global__ __launch_bounds__(256) void batch_rope_half_kernel(const float *__res
                                                               const float *__restrict__ v, float *__restrict__ qr,
                                                               _Float16 *__restrict__ kc, _Float16 *__restrict__ vc,
                                                               uint32_t rows, uint32_t pos, float theta) {
-    __shared__ float inv_freq[32];
-    fill_inv_freq(inv_freq, theta);
-    __syncthreads();
+    const float ifreq = lane_inv_freq(theta);
     const int lane = threadIdx.x & 63;
     const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;                                         // wave-uniform
-    const Rope4 r = rope_angles(pos + row, lane, inv_freq);
+    const Rope4 r = rope_angles(pos + row, lane, ifreq);
     typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 #pragma unroll 4
     for (int h = 0; h < 16; h++) {
