@@ -199,7 +199,8 @@ def run_decode(device, q, gate, cache, rows, history, path="fused", length_cap=N
     return y
 
 
-DECODE_CASES = [(0, 1), (1, 1), (17, 7), (127, 1), (255, 1), (256, 1), (4093, 7), (8191, 1), (30000, 1), (65535, 2)]
+DECODE_CASES = [(0, 1), (1, 1), (17, 7), (127, 1), (255, 1), (256, 1), (1000, 64), (4093, 7), (8191, 1), (30000, 1),
+                (65535, 2)]
 
 
 @pytest.mark.parametrize("path", ["fused", "reference"])
