@@ -325,10 +325,10 @@ def main():
     device.reset_wall_timing(kernels_exact=True)
     for _ in range(args.steps):
         control.step()
-    kc = kernel_stats(device, ["prefill_kernel<false>", "prefill_combine_kernel<128>", "batch_rope_half_kernel"])
+    kc = kernel_stats(device, ["prefill_fp16_kernel", "prefill_combine_kernel<128>", "batch_rope_half_kernel"])
     result["fp16_kv_control"] = {
         "ms_per_layer": round(fp16_ms, 4),
-        "attention_kernel_ms_per_layer": round(kc["prefill_kernel<false>"][0] / args.steps, 4),
+        "attention_kernel_ms_per_layer": round(kc["prefill_fp16_kernel"][0] / args.steps, 4),
         "combine_ms_per_layer": round(kc.get("prefill_combine_kernel<128>", (0.0, 0))[0] / args.steps, 4),
         "append_ms_per_layer": round(kc["batch_rope_half_kernel"][0] / args.steps, 4),
         "int8_over_fp16_time": round(wall_ms / fp16_ms, 4),

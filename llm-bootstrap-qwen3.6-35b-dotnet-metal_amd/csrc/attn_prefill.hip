@@ -18,19 +18,16 @@
 // Logical row r of KV group g is (token r/8, head 8g + r%8): the grouped FP16
 // query layout of attention_query_grouped_half (kernels.metal:1276-1281).
 //
-// gfx950 structure (not the Metal tiling): a work-group of 4 waves owns 128
-// logical rows (16 tokens x 8 heads) of one KV group, each wave 32 rows, and
-// two work-groups share a CU (two waves per SIMD) so that one work-group's MFMA
-// work overlaps the other's softmax VALU, LDS and memory latency. Per 64-key
-// step the work-group dequantizes the INT8 K tile and the V page slice to FP16
-// once into LDS (codes are exact), then every wave computes S^T = K . Q^T and
-// O^T += V^T . P^T with v_mfma_f32_32x32x16_f16. Transposed products put one
-// query row per lane column, so row statistics are per-lane and the
-// accumulator rescale needs no cross-lane traffic; the key order inside each
-// QK tile is permuted so a lane's S registers are exactly its FP16 B operand
-// for the PV product. The exponentials run in the base-2 domain (the K scale
-// carries log2(e)/16) against a lazy running maximum. Long histories split
-// the key range across work-groups (split-K) and a combine kernel merges
+// gfx950 structure (not the Metal tiling), shared by the INT8 kernel
+// (prefill_pp_kernel) and the FP16-KV control (prefill_fp16_kernel): every wave
+// owns 32 logical rows and computes S^T = K . Q^T and O^T += V^T . P^T with
+// v_mfma_f32_32x32x16_f16 on FP16 operands staged in LDS (INT8 codes are exact in
+// FP16). Transposed products put one query row per lane column, so row statistics
+// are per-lane and the accumulator rescale needs no cross-lane traffic; the key
+// order inside each QK tile is permuted so a lane's S registers are exactly its
+// FP16 B operand for the PV product. The exponentials run in the base-2 domain
+// (the K scale carries log2(e)/16) against a lazy running maximum. Long histories
+// split the key range across work-groups (split-K) and a combine kernel merges
 // (m, l, O); blocks sharing a key range are placed on the same XCD so its L2
 // serves their K/V tiles.
 #include "common.h"
@@ -72,22 +69,20 @@ __device__ inline float sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }
 __device__ inline int qk_key_row(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
 
 
-// kInt8: the INT8 cache (codes + FP32 per-token scales). Otherwise the FP16
-// token-major control cache of attention_online_q32_k256_s8_g8_r2
+// The FP16 token-major control cache of attention_online_q32_k256_s8_g8_r2
 // (kernels.metal:1356-1365): no scales, FP16 probabilities e (<= 2^8 with the lazy
-// maximum), V transposed into LDS by the staging loop.
-template <bool kInt8>
-__global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillParams p) {
+// maximum), V transposed into LDS by the staging loop. A work-group of 4 waves owns
+// 128 logical rows (16 tokens x 8 heads) of one KV group and two work-groups share a
+// CU (two waves per SIMD), so that one's MFMA work overlaps the other's softmax.
+__global__ __launch_bounds__(256, 2) void prefill_fp16_kernel(PrefillParams p) {
     __shared__ __attribute__((aligned(16))) _Float16 klds[kKeys * kKStride];
     __shared__ __attribute__((aligned(16))) _Float16 vlds[256 * kVStride];
     __shared__ float kscale[kKeys], vscale[kKeys];
-    __shared__ float vs_partial[4];
 
     // ---- block -> (group, tile, split); XCD-aware: blocks sharing a key range
     // (same group and split) land on the same XCD (round-robin dispatch).
     uint32_t b = blockIdx.x, g, tile, split;
     {
-        const uint32_t combos = 2 * p.splits;
         uint32_t combo;
         if (p.remap) {
             const uint32_t xcd = b % 8, idx = b / 8;
@@ -97,7 +92,6 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillParams p) {
             combo = b / p.tiles;
             tile = b % p.tiles;
         }
-        (void)combos;
         g = combo % 2;
         split = combo / 2;
     }
@@ -124,17 +118,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillParams p) {
         for (int c = 0; c < 16; c++) qop[c] = *reinterpret_cast<const half8 *>(qrow + 16 * c);
     }
 
-    // ---- vs_ref: the largest V scale over this block's keys (0 if all are 0)
     const int tid = threadIdx.x;
-    float vs_ref = kInt8 ? 0.0f : 1.0f;
-    if (kInt8)
-        for (uint32_t key = kbeg + tid; key < kend; key += 256) vs_ref = fmaxf(vs_ref, p.vs[(size_t)key * 2 + g]);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) vs_ref = fmaxf(vs_ref, __shfl_xor(vs_ref, o, 64));
-    if (lane == 0) vs_partial[wave] = vs_ref;
-    __syncthreads();
-    vs_ref = fmaxf(fmaxf(vs_partial[0], vs_partial[1]), fmaxf(vs_partial[2], vs_partial[3]));
-    const float vs_inv = vs_ref > 0.0f ? 1.0f / vs_ref : 0.0f;
 
     floatx16 o[8];
 #pragma unroll
@@ -145,9 +129,9 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillParams p) {
 
     for (uint32_t key0 = kbeg; key0 < kend; key0 += kKeys) {
         __syncthreads();   // previous tile fully consumed
-        // ---- stage K: 64 keys x 256 codes -> FP16; thread: key key0 + tid/4, 64 codes
-        if (!kInt8) {
-            // FP16 control: K rows copied as they are, V rows transposed into V^T
+        // ---- stage 64 keys: K rows copied as they are, V rows transposed into V^T;
+        // thread: key key0 + tid/4, 64 values
+        {
             const int krow = tid >> 2, part = tid & 3;
             const uint32_t key = min(key0 + krow, p.keys - 1);
             const uint4 *ksrc = reinterpret_cast<const uint4 *>((const _Float16 *)p.k + ((size_t)key * 2 + g) * 256 + part * 64);
@@ -162,50 +146,11 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillParams p) {
 #pragma unroll
                 for (int e = 0; e < 8; e++) vlds[(part * 64 + 8 * j + e) * kVStride + krow] = hv[e];
             }
-        } else {
-            const int krow = tid >> 2, part = tid & 3;
-            const uint32_t key = min(key0 + krow, p.keys - 1);
-            const uint4 *src = reinterpret_cast<const uint4 *>((const int8_t *)p.k + ((size_t)key * 2 + g) * 256 + part * 64);
-            uint4 *dst = reinterpret_cast<uint4 *>(klds + krow * kKStride);
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint4 w = src[j];
-                uint32_t h[8];
-                i8x4_to_f16(w.x, h[0], h[1]);
-                i8x4_to_f16(w.y, h[2], h[3]);
-                i8x4_to_f16(w.z, h[4], h[5]);
-                i8x4_to_f16(w.w, h[6], h[7]);
-                dst[part * 8 + 2 * j] = make_uint4(h[0], h[1], h[2], h[3]);
-                dst[part * 8 + 2 * j + 1] = make_uint4(h[4], h[5], h[6], h[7]);
-            }
-        }
-        // ---- stage V^T: 256 dims x 64 keys of the page slice -> FP16
-        if (kInt8) {
-            const int8_t *page = (const int8_t *)p.v + value_index((uint64_t)key0 * 2 + g, 0);
-#pragma unroll
-            for (int it = 0; it < 4; it++) {
-                const int d = it * 64 + (tid >> 2), part = tid & 3;
-                const uint4 w = *reinterpret_cast<const uint4 *>(page + (size_t)d * 256 + part * 16);
-                uint32_t h[8];
-                i8x4_to_f16(w.x, h[0], h[1]);
-                i8x4_to_f16(w.y, h[2], h[3]);
-                i8x4_to_f16(w.z, h[4], h[5]);
-                i8x4_to_f16(w.w, h[6], h[7]);
-                uint4 *dst = reinterpret_cast<uint4 *>(vlds + d * kVStride + part * 16);
-                dst[0] = make_uint4(h[0], h[1], h[2], h[3]);
-                dst[1] = make_uint4(h[4], h[5], h[6], h[7]);
-            }
         }
         if (tid < kKeys) {
-            const uint32_t key = key0 + tid;
-            const bool inside = key < p.keys;   // poisoned tails beyond K never reach P
-            if (kInt8) {
-                kscale[tid] = inside ? p.ks[(size_t)key * 2 + g] * (kLog2e / 16.0f) : 0.0f;
-                vscale[tid] = inside ? p.vs[(size_t)key * 2 + g] * vs_inv : 0.0f;
-            } else {
-                kscale[tid] = kLog2e / 16.0f;
-                vscale[tid] = inside ? 1.0f : 0.0f;
-            }
+            const bool inside = key0 + tid < p.keys;   // poisoned tails beyond K never reach P
+            kscale[tid] = kLog2e / 16.0f;
+            vscale[tid] = inside ? 1.0f : 0.0f;
         }
         __syncthreads();
 
@@ -285,7 +230,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillParams p) {
         if (!row_valid) return;
         const uint32_t token = my_row / 8, head = g * 8 + my_row % 8;
         const size_t base = ((size_t)token * 16 + head) * 256;
-        const float inv = vs_ref / l;
+        const float inv = 1.0f / l;
 #pragma unroll
         for (int dt = 0; dt < 8; dt++)
 #pragma unroll
@@ -303,8 +248,6 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillParams p) {
     }
     float *part = p.partial + (((size_t)g * p.tiles + tile) * p.splits + split) * kPartialStride;
     const int local_row = 32 * wave + i;
-#pragma unroll
-    for (int dt = 0; dt < 8; dt++) o[dt] *= vs_ref;
 #pragma unroll
     for (int dt = 0; dt < 8; dt++)
 #pragma unroll
@@ -908,7 +851,7 @@ const char *launch_prefill(Context &c, const View *b, int count, const boot_kern
     if (int8)
         launch_timed(c, "prefill_pp_kernel", prefill_pp_kernel, dim3((uint32_t)blocks), dim3(512), p);
     else
-        launch_timed(c, "prefill_kernel<false>", prefill_kernel<false>, dim3((uint32_t)blocks), dim3(256), p);
+        launch_timed(c, "prefill_fp16_kernel", prefill_fp16_kernel, dim3((uint32_t)blocks), dim3(256), p);
     if (splits > 1) {
         context_split(c, int8 ? "attention_online_int8.combine" : "attention_online_fp16.combine");
         if (int8)
