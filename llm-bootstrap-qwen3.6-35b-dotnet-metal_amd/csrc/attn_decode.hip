@@ -191,10 +191,10 @@ __device__ __attribute__((always_inline)) inline uint4 load_k_piece(const Decode
     return *reinterpret_cast<const uint4 *>(p.k + ((size_t)t * 2 + g) * 256 + 16 * (tid & 15));
 }
 
-// Chunk idx of the split starting at token `begin`. Past the last chunk the loads
-// stay (a fixed count keeps the counter waits exact) but every lane reads the same
-// 16 bytes of the first one: a cache line instead of a 64 KB re-read that the
-// epilogue would wait for.
+// Chunk idx of the split starting at token `begin`. Past the last chunk (only the
+// prologue's loads of a split shorter than three chunks) the loads stay, a fixed
+// count that keeps the counter waits exact, but every lane reads the same 16 bytes
+// of the first one: a cache line instead of a 64 KB re-read.
 __device__ __attribute__((always_inline)) inline void load_chunk(ChunkRegs &r, const DecodeParams &p, uint32_t g,
                                                                  uint32_t begin, uint32_t idx, uint32_t nchunks,
                                                                  uint32_t length, int tid) {
