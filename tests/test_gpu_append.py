@@ -167,3 +167,36 @@ def test_dispatch_validation_errors(device):
     with pytest.raises(HipError, match="requires an active command"):
         device.dispatch("kv_store_int8", KernelArgs(M=1), 1, 1, small)
     small.dispose()
+
+
+def test_attention_dispatch_validation_errors(device):
+    """The attention launchers reject, on the host and before any launch, what the
+    reference's call sites never pass: a group size other than 8, K != Position + M,
+    a history beyond the 262144-token window, missing or undersized or misaligned
+    bindings, and more than 64 decode rows."""
+    from bootstrap_hip import HipError
+    rows, pos = 4, 100
+    keys = pos + rows
+    q = device.allocate(rows * 8192 + 64)
+    cache_k, cache_v = device.allocate(keys * 512), device.allocate((keys + 255) // 256 * 256 * 512)
+    gate, y = device.allocate(rows * 16384), device.allocate(rows * 16384)
+    ks, vs = device.allocate(keys * 8), device.allocate(keys * 8)
+    name = "attention_online_int8_q32_k256_r2"
+    bind = (q, cache_k, cache_v, gate, y, ks, vs)
+    cases = [
+        (name, KernelArgs(M=rows, K=keys, Position=pos, A=4), bind, "A = 8"),
+        (name, KernelArgs(M=rows, K=keys + 1, Position=pos, A=8), bind, "K must equal"),
+        (name, KernelArgs(M=1, K=262145, Position=262144, A=8), bind, "262144-token window"),
+        (name, KernelArgs(M=rows, K=keys, Position=pos, A=8), bind[:6], "needs 7 bindings"),
+        (name, KernelArgs(M=rows, K=keys, Position=pos, A=8), (ks,) + bind[1:], "query smaller"),
+        (name, KernelArgs(M=rows, K=keys, Position=pos, A=8), (q.at(4),) + bind[1:], "misaligned"),
+        ("attention_decode_int8", KernelArgs(M=65, K=keys, Position=pos), bind, "at most 64 rows"),
+        ("attention_decode_int8", KernelArgs(M=rows, K=keys, Position=pos), bind[:6], "needs 7 bindings"),
+    ]
+    for kernel, args, bindings, message in cases:
+        device.begin()
+        with pytest.raises(HipError, match=message):
+            device.dispatch(kernel, args, rows * 4096, 256, *bindings)
+        device.end()
+    for b in bind:
+        b.dispose()
