@@ -34,6 +34,7 @@ __global__ __launch_bounds__(64) void scores_int8_kernel(const float *__restrict
                                                          uint32_t rows, uint32_t K, uint32_t pos) {
     __shared__ float qs[8][256];
     const uint32_t row = blockIdx.y >> 1, g = blockIdx.y & 1;
+    if (row >= rows) return;
     for (int i = threadIdx.x; i < 8 * 256; i += 64) qs[i / 256][i % 256] = q[(size_t)row * 4096 + (g * 8) * 256 + i];
     __syncthreads();
     const uint32_t t = blockIdx.x * 64 + threadIdx.x;

@@ -793,7 +793,7 @@ inline bool aligned(const void *ptr, uintptr_t a) { return (reinterpret_cast<uin
 
 namespace {
 
-const char *launch_prefill(Context &c, const View *b, int count, const boot_kernel_args &a, bool int8) {
+const char *launch_prefill(Context &c, const View *b, const boot_kernel_args &a, bool int8) {
     const uint64_t rows = a.m;
     if (rows == 0) return nullptr;
     BOOT_REQUIRE(a.a == 8 || a.a == 0, "online attention groups 8 query heads per KV head (A = 8)");
@@ -868,13 +868,13 @@ const char *launch_online_int8(Context &c, const View *b, int count, const boot_
     // bindings (DeviceAttention.cs:69): q FP16 grouped, k, v, gate, y, ks, vs; M rows, K = pos + M,
     // Position = pos, A = 8 heads per group.
     BOOT_REQUIRE(count >= 7, "attention_online_int8 needs 7 bindings: q, k, v, gate, y, ks, vs");
-    return launch_prefill(c, b, count, a, true);
+    return launch_prefill(c, b, a, true);
 }
 
 const char *launch_online_fp16(Context &c, const View *b, int count, const boot_kernel_args &a, const uint32_t *) {
     // bindings (DeviceAttention.cs:62-63): q FP16 grouped, k FP16, v FP16 (token-major), gate, y
     BOOT_REQUIRE(count >= 5, "attention_online_q32_k256_s8_g8_r2 needs 5 bindings: q, k, v, gate, y");
-    return launch_prefill(c, b, count, a, false);
+    return launch_prefill(c, b, a, false);
 }
 
 }  // namespace boot
