@@ -12,6 +12,7 @@ HIP shim so the device path can be driven the way the engine drives it:
 * ``DeviceAttentionWorkspace`` DeviceAttention.cs:14-20 (Prepare), 65-70 (EncodeInt8)
 * ``append_rows`` / ``decode`` the INT8 lines of PrefillBlock (Prefill.cs:248-261) and
                                Forward (QwenEngine.cs:158-166)
+* ``verify_attention_int8``    the verify-block reader of PrefillBlock (Prefill.cs:269-285)
 """
 from __future__ import annotations
 
@@ -282,3 +283,35 @@ def decode_reference_path(device: Device, layer: Int8KvLayer, rotated, gate, out
     device.dispatch("attention_softmax", soft, rows * 16 * 256, 256, scores)
     device.dispatch("batch_attention_values_int8", p, rows * 4096, 128, scores, layer.value, gate, output,
                     layer.value_scale)
+
+
+def verify_slices(rows: int, position: int,
+                  workspace_floats: int = ATTENTION_WORKSPACE_FLOATS) -> List[tuple]:
+    """Query slices of a verify block (Prefill.cs:273-276): as many rows per slice as keep
+    rows*16*(position+rows_total) score floats inside the workspace; (first, count) pairs."""
+    length = position + rows
+    capacity = workspace_floats // 16 // length
+    if rows < 1 or capacity < 1:
+        raise ValueError("Attention workspace budget exceeded")
+    return [(first, min(capacity, rows - first)) for first in range(0, rows, capacity)]
+
+
+def verify_attention_int8(device: Device, layer: Int8KvLayer, rotated: GpuBuffer, gate: GpuBuffer,
+                          scores: GpuBuffer, rows: int, position: int,
+                          workspace_floats: int = ATTENTION_WORKSPACE_FLOATS) -> None:
+    """INT8 attention of a speculative verify block (Prefill.cs:269-285, ``verify`` true): the
+    scalar reader over query slices. Each slice keeps its absolute causal position and the whole
+    block's key count as the score stride, and writes its output over its own rotated query rows.
+    Inside a command."""
+    length = position + rows
+    for first, count in verify_slices(rows, position, workspace_floats):
+        if scores.length < count * 16 * length * 4:
+            raise ValueError("score workspace smaller than one slice")
+        p = KernelArgs(M=count, K=length, Position=position + first)
+        query, g = rotated.at(first * 4096 * 4), gate.at(first * 4096 * 4)
+        device.dispatch2d("batch_attention_scores_int8", p, length * 32, count * 16, 128, query, layer.key, scores,
+                          layer.key_scale)
+        soft = KernelArgs(M=count, K=length, Position=length - 1)
+        device.dispatch("attention_softmax", soft, count * 16 * 256, 256, scores)
+        device.dispatch("batch_attention_values_int8", p, count * 4096, 128, scores, layer.value, g, query,
+                        layer.value_scale)

@@ -70,3 +70,17 @@ def test_target_kv_bytes_full_window():
     total = cap * 512 * 2 * layers + cap * 2 * 2 * layers * 4 + (int8_value_capacity(cap) - cap) * 512 * layers
     assert total == 2_726_297_600
     assert int8_value_capacity(4097) == 4352 and int8_value_capacity(4096) == 4096
+
+
+def test_verify_slices_follow_the_workspace_budget():
+    from bootstrap_hip import engine
+    # Prefill.cs:273-276: rows per slice = AttentionWorkspaceFloats / 16 / (position + count)
+    assert engine.verify_slices(8, 262136) == [(0, 8)]                        # full window: 8 rows fit
+    slices = engine.verify_slices(512, 30208)                                 # 2097152 // 30720 = 68
+    assert [n for _, n in slices] == [68] * 7 + [36]
+    assert [f for f, _ in slices] == list(range(0, 512, 68))
+    assert engine.verify_slices(5, 0, workspace_floats=16 * 5 * 2) == [(0, 2), (2, 2), (4, 1)]
+    with pytest.raises(ValueError):
+        engine.verify_slices(8, 100, workspace_floats=16 * 100)               # not one row fits
+    with pytest.raises(ValueError):
+        engine.verify_slices(0, 100)
