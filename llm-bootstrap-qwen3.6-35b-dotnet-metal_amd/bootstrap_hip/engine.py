@@ -13,6 +13,8 @@ HIP shim so the device path can be driven the way the engine drives it:
 * ``append_rows`` / ``decode`` the INT8 lines of PrefillBlock (Prefill.cs:248-261) and
                                Forward (QwenEngine.cs:158-166)
 * ``verify_attention_int8``    the verify-block reader of PrefillBlock (Prefill.cs:269-285)
+* ``PrefixLineage``            checkpoint index of the single KV lineage (PrefixCache.cs:8-122,
+                               QwenEngine.cs:195-233), KV part
 """
 from __future__ import annotations
 
@@ -169,6 +171,130 @@ class Int8KvCache:
             h.update(layer.key_scale.read(np.uint8, consumed * 8).tobytes())
             h.update(layer.value_scale.read(np.uint8, consumed * 8).tobytes())
         return h.hexdigest()
+
+
+# PrefixCache.cs:8
+PREFIX_CHECKPOINT_LIMIT, PREFIX_CHECKPOINT_INTERVAL = 4, 4096
+
+
+class PrefixLineage:
+    """Checkpoint index of the single live KV lineage (PrefixCache.cs:8-122 and the prompt loop
+    of QwenEngine.cs:195-233), KV part. A checkpoint is a position of that lineage: the codes and
+    scales stay in place in the device store, and restoring one truncates the lineage by position
+    (``Int8KvCache.restore_prefix``); nothing past it is cleared, since every position consumed
+    later is overwritten before a causal read. The recurrent/conv/logit snapshot the reference
+    stores with each checkpoint belongs to the model's other layers and is not kept here.
+    ``end_token`` is the tokenizer's message-end id (Tokenizer.cs:19)."""
+
+    def __init__(self, cache: Int8KvCache, end_token: int, limit: int = PREFIX_CHECKPOINT_LIMIT,
+                 interval: int = PREFIX_CHECKPOINT_INTERVAL):
+        self.cache = cache
+        self.end_token = end_token
+        self.limit, self.interval = limit, interval
+        self.checkpoints: List[int] = []     # positions, in the order saved (PrefixCache.cs:12)
+        self.tokens: List[int] = []          # the prompt the lineage was built from (PrefixCache.cs:14)
+        self._enabled = True
+
+    @property
+    def enabled(self) -> bool:
+        return self._enabled
+
+    @enabled.setter
+    def enabled(self, value: bool) -> None:
+        """PrefixCache.cs:16-20: toggling drops every checkpoint."""
+        if self._enabled != value:
+            self.clear()
+        self._enabled = value
+
+    def clear(self) -> None:
+        """ClearPrefixCache (PrefixCache.cs:28-32)."""
+        self.checkpoints = []
+        self.tokens = []
+
+    def reset(self) -> None:
+        """QwenEngine.cs:122-131, KV part: drop the checkpoints and clear the store."""
+        self.clear()
+        self.cache.reset()
+
+    def find(self, prompt) -> Optional[int]:
+        """FindPrefix (PrefixCache.cs:34-40): the last saved checkpoint inside the prompt's common
+        prefix with the lineage's prompt."""
+        if not self._enabled:
+            return None
+        common, limit = 0, min(len(prompt), len(self.tokens))
+        while common < limit and prompt[common] == self.tokens[common]:
+            common += 1
+        hits = [c for c in self.checkpoints if c <= common]
+        return hits[-1] if hits else None
+
+    def cached_tokens(self, prompt) -> int:
+        """CachedPrefixTokens (PrefixCache.cs:42)."""
+        found = self.find(prompt)
+        return 0 if found is None else found
+
+    def restore(self, prompt) -> int:
+        """RestorePrefix (PrefixCache.cs:45-77), KV part: no checkpoint resets the lineage;
+        otherwise checkpoints past the one found are dropped before the first write and the
+        lineage is truncated to it. Returns the position prefill resumes from."""
+        checkpoint = self.find(prompt)
+        if checkpoint is None:
+            self.reset()
+            return 0
+        while self.checkpoints and self.checkpoints[-1] > checkpoint:
+            self.checkpoints.pop()
+        return self.cache.restore_prefix(checkpoint)
+
+    def boundaries(self, prompt) -> List[int]:
+        """PrefixBoundaries (PrefixCache.cs:107-122): prompt end, end of the first and of the
+        last message, then whole checkpoint-interval blocks from the latest down, at most
+        ``limit`` positions."""
+        n = len(prompt)
+        found = {n}
+        ends = [i for i, t in enumerate(prompt) if t == self.end_token]
+        first_message = ends[0] + 1 if ends else 0
+        last_message = ends[-1] + 1 if ends else 0
+        if first_message > 0:
+            found.add(first_message)
+        if last_message > 0:
+            found.add(last_message)
+        block = (n - 1) // self.interval * self.interval
+        while block > 0 and len(found) < self.limit:
+            found.add(block)
+            block -= self.interval
+        return sorted(found)
+
+    def save(self, position: int, boundaries: List[int]) -> None:
+        """SavePrefix (PrefixCache.cs:79-105), KV part: at the limit, evict the first checkpoint
+        that is not one of this request's boundaries (else the oldest)."""
+        if not self._enabled or position in self.checkpoints:
+            return
+        if len(self.checkpoints) == self.limit:
+            victims = [i for i, c in enumerate(self.checkpoints) if c not in boundaries]
+            del self.checkpoints[victims[0] if victims else 0]
+        self.checkpoints.append(position)
+
+    def begin(self, prompt) -> tuple:
+        """The head of Generate (QwenEngine.cs:201-206): restore, then own a copy of the prompt
+        as the lineage key. Returns (position, boundaries)."""
+        position = self.restore(prompt)
+        boundaries = self.boundaries(prompt)
+        self.tokens = list(prompt) if self._enabled else []
+        return position, boundaries
+
+    @staticmethod
+    def plan(prompt_length: int, position: int, boundaries: List[int]) -> List[tuple]:
+        """The batched prompt loop of QwenEngine.cs:207-233 (WidePrefill off): chunks of
+        ``ContextLimits.prefill_count`` rows that never cross a boundary; a chunk under 8 rows
+        runs one token at a time. (position, rows, checkpoint-after) triples."""
+        chunks = []
+        while position < prompt_length:
+            boundary = next(p for p in boundaries if p > position)
+            count = ContextLimits.prefill_count(position, boundary - position)
+            if count < 8:
+                count = 1
+            chunks.append((position, count, position + count == boundary))
+            position += count
+        return chunks
 
 
 class DeviceAttentionWorkspace:
