@@ -45,8 +45,10 @@ def run_prefill(device, q, gate, cache, rows, history, alias=False, kernel="atte
     return y
 
 
+# the last two: config 3's final chunk at full size, and a block ending exactly at the
+# 262144-token window (ContextLimits.cs:5)
 PREFILL_CASES = [(0, 1), (17, 7), (127, 31), (127, 32), (257, 33), (4093, 7), (8192, 128), (0, 512), (3584, 512),
-                 (30000, 33)]
+                 (30000, 33), (30208, 512), (262080, 64)]
 
 
 @pytest.mark.parametrize("history,rows", PREFILL_CASES)
