@@ -125,7 +125,6 @@ constexpr int kDecodeWaves = 8;
 constexpr int kMaxSplitTokens = 2048;            // tokens per work-group at most (LDS scales)
 constexpr int kPartialFloats = 8 * 256 + 16;    // O[8][256], m[8], l[8] per (row, group, split)
 constexpr int kMaxDecodeSplits = 1024;
-constexpr int kMergeStride = 256 + 16;            // merge row (floats): the 8 heads of a write spread over the banks
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct DecodeParams {
@@ -233,22 +232,23 @@ __device__ __attribute__((always_inline)) inline void store_chunk(ChunkLds &b, c
 // Grid: (splits, 2 KV groups, rows), one 8-wave work-group per CU; a split is
 // split_chunks chunks of 128 tokens, chosen on the host so that the grid fits the
 // CUs in one round. The work-group streams its chunks through double-buffered LDS
-// with two chunks in flight in registers; per chunk wave w takes tokens 16w..16w+15:
+// with two chunks in flight in registers. Per chunk wave w scores tokens 16w..16w+15,
 // S^T[t][n] = K[t] . Qx[n] (16x16x64 INT8 MFMA on the raw K codes, n = 8 heads x
-// {q1, q2}), the online softmax of the 8 heads in base 2, and
-// O^T[d][n] += V^T[d][t] . Px[t][n] (16x16x16 FP16 MFMA) with Px = p * vs / vs_ref
-// split into FP16 hi + lo; vs_ref, the split's largest V scale, keeps Px in [0, 1]
-// and multiplies the result once. Lane l holds MFMA column n = l % 16 and
+// {q1, q2}), and turns them into probabilities in base 2 against a running reference
+// shared by the work-group; the waves exchange those P operands through LDS and wave w
+// accumulates O^T[d][n] += V^T[d][t] . Px[t][n] for dimensions 32w..32w+31 over all 128
+// tokens (16x16x16 FP16 MFMA), so no wave merge of O remains at the end. Px = p * vs /
+// vs_ref split into FP16 hi + lo; vs_ref, the split's largest V scale, keeps Px below
+// 256 and multiplies the result once. Lane l holds MFMA column n = l % 16 and
 // token/k group qq = l / 16.
 __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
     typedef int v4i __attribute__((ext_vector_type(4)));
     typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-    // the chunk buffers; after the last chunk the same bytes hold the wave merge
+    // the chunk buffers
     __shared__ __attribute__((aligned(16))) unsigned char arena[2 * sizeof(ChunkLds)];
-    static_assert(sizeof(float) * kDecodeWaves * 8 * kMergeStride <= 2 * sizeof(ChunkLds), "merge buffer exceeds the arena");
     ChunkLds *bufs = reinterpret_cast<ChunkLds *>(arena);
-    auto merge_o = reinterpret_cast<float (*)[8][kMergeStride]>(arena);
-    __shared__ float merge_m[kDecodeWaves][8], merge_l[kDecodeWaves][8];
+    __shared__ float chunk_top[kDecodeWaves][16], wave_l[kDecodeWaves][16];
+    __shared__ uint2 pshare[kDecodeWaves][64];   // each wave's P operand of the chunk
     __shared__ float kscale[kMaxSplitTokens], vscale[kMaxSplitTokens];
     __shared__ float red[kDecodeWaves], qmax[4][8];
     __shared__ v4i qlds[4][64];    // INT8 query operands, [MFMA c][lane]
@@ -343,9 +343,9 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
 #pragma unroll
     for (int c = 0; c < 4; c++) qi[c] = qlds[c][lane];
 
-    floatx4 o[16];
-#pragma unroll
-    for (int i = 0; i < 16; i++) o[i] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    floatx4 o[2];   // O^T tiles dt = 2 wave + i, over every token of the split
+    o[0] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    o[1] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     float m = -INFINITY, l = 0.0f;
 
     // one chunk from LDS: QK, the online softmax, PV
@@ -371,38 +371,58 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
         }
         top = fmaxf(top, __shfl_xor(top, 16, 64));
         top = fmaxf(top, __shfl_xor(top, 32, 64));
-        const float next = fmaxf(m, top);
-        // a wave whose tokens are all past the split end keeps m = -inf: no decay
-        const float decay = next == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - next);
-        float total = 0.0f;
-        _Float16 hv[4];
+        // the waves share one running reference m per column; a chunk rescales (and pays a
+        // second barrier) only when some column's maximum passes m by more than 2^8, so
+        // p = 2^(s - m) stays below 256
+        auto probs = [&](float ref, float &total) {
+            _Float16 hv[4];
+            total = 0.0f;
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const float prob = next == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc[r] - next);   // 0 for masked tokens
-            total += prob;
-            const float scaled = prob * (vscale[local0 + r] * vs_inv);
-            const _Float16 hi = (_Float16)scaled;
-            hv[r] = lo_col ? (_Float16)(scaled - (float)hi) : hi;
+            for (int r = 0; r < 4; r++) {
+                const float prob = ref == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc[r] - ref);   // 0 for masked tokens
+                total += prob;
+                const float scaled = prob * (vscale[local0 + r] * vs_inv);
+                const _Float16 hi = (_Float16)scaled;
+                hv[r] = lo_col ? (_Float16)(scaled - (float)hi) : hi;
+            }
+            total += __shfl_xor(total, 16, 64);
+            total += __shfl_xor(total, 32, 64);
+            const half4 pop = {hv[0], hv[1], hv[2], hv[3]};
+            pshare[wave][lane] = __builtin_bit_cast(uint2, pop);
+        };
+        float total;
+        probs(m, total);
+        if (qq == 0) chunk_top[wave][n] = top;
+        __syncthreads();
+        float ctop = chunk_top[0][n];
+#pragma unroll
+        for (int w = 1; w < kDecodeWaves; w++) ctop = fmaxf(ctop, chunk_top[w][n]);
+        // every wave reads the same maxima: the branch is uniform over the work-group
+        if (__builtin_amdgcn_ballot_w64(ctop > m + 8.0f) != 0) {
+            const float next = fmaxf(m, ctop);
+            const float decay = next == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - next);
+            l *= decay;
+            o[0] *= decay;
+            o[1] *= decay;
+            m = next;
+            probs(m, total);   // no wave reads P before this branch
+            __syncthreads();
         }
-        total += __shfl_xor(total, 16, 64);
-        total += __shfl_xor(total, 32, 64);
-        l = l * decay + total;
-        m = next;
-        if (decay != 1.0f) {
+        l += total;   // this wave's tokens
+        // O^T[d][n] += V^T[d][t] P[t][n] for this wave's 32 dimensions over the chunk's 128
+        // tokens: k-step src takes wave src's tokens 16 src..16 src+15 and P operand
 #pragma unroll
-            for (int i = 0; i < 16; i++) o[i] *= decay;
-        }
-        const half4 pop = {hv[0], hv[1], hv[2], hv[3]};
-        // V^T operand: row d = 16dt + n, the 4 codes of tokens 16w + 4qq + [0, 4)
-        const int vpiece = wave;   // tokens 16w..16w+15
+        for (int src = 0; src < kDecodeWaves; src++) {
+            const half4 ps = __builtin_bit_cast(half4, pshare[src][lane]);
 #pragma unroll
-        for (int dt = 0; dt < 16; dt++) {
-            const int d = 16 * dt + n;
-            const uint32_t w4 = reinterpret_cast<const uint32_t *>(&b.v[d][vpiece ^ ((d >> 1) & 7)])[qq];
-            uint32_t h0, h1;
-            i8x4_to_f16(w4, h0, h1);
-            const half4 va = __builtin_bit_cast(half4, make_uint2(h0, h1));
-            o[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pop, o[dt], 0, 0, 0);
+            for (int j = 0; j < 2; j++) {
+                const int d = 16 * (2 * wave + j) + n;
+                const uint32_t w4 = reinterpret_cast<const uint32_t *>(&b.v[d][src ^ ((d >> 1) & 7)])[qq];
+                uint32_t h0, h1;
+                i8x4_to_f16(w4, h0, h1);
+                const half4 va = __builtin_bit_cast(half4, make_uint2(h0, h1));
+                o[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, ps, o[j], 0, 0, 0);
+            }
         }
     };
     // Chunks in pairs, so that the two register sets take turns without copies (a
@@ -443,54 +463,26 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
             }
         }
     }
-    __syncthreads();
 
-    // ---- merge the eight waves: O^T[d][n] with d = 16*dt + 4*qq + r; heads sum hi + lo columns;
-    // statistics are in base 2, O in units of vs_ref. The arena is free: the chunks
-    // ended with a barrier and none is read again.
-    // the lo column n + 8 of each head joins its hi column n in registers, then the
-    // hi lanes publish the head. The DPP adds take MFMA results as inline-assembly
-    // operands, for which the compiler inserts no wait states: cover them here.
+    // ---- the waves share m; l sums over waves. O^T[d][n], d = 16 dt + 4 qq + r: the lo
+    // column n + 8 of each head joins its hi column n in registers (the DPP adds take MFMA
+    // results as inline-assembly operands, for which the compiler inserts no wait states:
+    // cover them here), then lanes n < 8 hold tile 2 wave and lanes n >= 8 tile 2 wave + 1.
+    if (qq == 0) wave_l[wave][n] = l;
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int dt = 0; dt < 16; dt += 2) add_row_partner8(o[dt], o[dt + 1]);
-    {
-        // lanes n and n + 8 now hold the same sums: each half of the row writes half of them
-        const bool upper = n >= 8;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const floatx4 val = upper ? o[8 + j] : o[j];
-            *reinterpret_cast<floatx4 *>(&merge_o[wave][head][16 * (j + (upper ? 8 : 0)) + 4 * qq]) = val;
-        }
-        if (n < 8 && qq == 0) {
-            merge_m[wave][head] = m;
-            merge_l[wave][head] = l;
-        }
-    }
+    add_row_partner8(o[0], o[1]);
     __syncthreads();
-    // thread -> (head h, 4 dims); combine waves with their maxima
-    const int h = threadIdx.x >> 6, d0 = (threadIdx.x & 63) * 4;
-    float mw = -INFINITY;
-    for (int w = 0; w < kDecodeWaves; w++) mw = fmaxf(mw, merge_m[w][h]);
-    float lw = 0.0f, f[kDecodeWaves];
-    for (int w = 0; w < kDecodeWaves; w++) {
-        f[w] = merge_m[w][h] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(merge_m[w][h] - mw);
-        lw += merge_l[w][h] * f[w];
-    }
-    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int w = 0; w < kDecodeWaves; w++) {
-        const float4 ow = *reinterpret_cast<const float4 *>(&merge_o[w][h][d0]);
-        acc.x += ow.x * f[w];
-        acc.y += ow.y * f[w];
-        acc.z += ow.z * f[w];
-        acc.w += ow.w * f[w];
-    }
-    acc.x *= vs_ref;
-    acc.y *= vs_ref;
-    acc.z *= vs_ref;
-    acc.w *= vs_ref;
+    float lw = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kDecodeWaves; w++) lw += wave_l[w][head];
+    const bool upper = n >= 8;
+    const int d0 = 16 * (2 * wave + (upper ? 1 : 0)) + 4 * qq;
+    const int h = head;
+    const float mw = m;
+    floatx4 res = upper ? o[1] : o[0];
+    float4 acc = make_float4(res[0] * vs_ref, res[1] * vs_ref, res[2] * vs_ref, res[3] * vs_ref);
     if (p.splits == 1) {
         // gate and y need only 4-byte alignment
         const size_t at = ((size_t)row * 16 + g * 8 + h) * 256 + d0;
@@ -503,7 +495,7 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
     }
     float *part = p.partial + (((size_t)row * 2 + g) * p.splits + split) * kPartialFloats;
     *reinterpret_cast<float4 *>(part + h * 256 + d0) = acc;
-    if ((threadIdx.x & 63) == 0) {
+    if (wave == 0 && lane < 8) {
         part[2048 + h] = mw;
         part[2056 + h] = lw;
     }

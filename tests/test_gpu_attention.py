@@ -222,6 +222,34 @@ def test_decode_matches_fp64(device, oracle, history, rows, path):
     cache.dispose()
 
 
+@pytest.mark.parametrize("history,rows,spikes", [
+    # a 131072-token context: 1152-token splits of nine 128-token chunks, spikes in later
+    # chunks of the first split, mid-context and at the end
+    (131071, 1, (5, 200, 300, 700, 1000, 1151, 60000, 60130, 131000, 131071)),
+    # several rows, spikes inside the block's own causal ends
+    (4093, 7, (5, 200, 1000, 4094, 4096, 4099)),
+])
+def test_decode_score_spikes(device, oracle, history, rows, spikes):
+    """Single keys whose scores jump far (tens of log2 units) above every earlier key, each
+    outgrowing the last: a work-group's shared running maximum must rebase between chunks."""
+    length = history + rows
+    q = (np.abs(oracle.fill_hash(rows * 4096, 17, 3)) + np.float32(0.25)).astype(np.float32)
+    k, v = reference_kv(length)
+    k = k / 3
+    for j, token in enumerate(spikes):
+        k[token] += np.float32(1.0 + 0.5 * j)
+    kc, vc, ks, vs = oracle.empty_cache(length + 1)
+    oracle.store(np.ascontiguousarray(k), v, 0, kc, vc, ks, vs)
+    poison_tail(oracle, kc, vc, ks, vs, length)
+    gate = oracle.fill_hash(rows * 4096, 11, 1)
+    cache = upload_cache(device, kc, vc, ks, vs)
+    y = run_decode(device, q, gate, cache, rows, history)[:-1]
+    assert np.all(np.isfinite(y))
+    ref = oracle.attention(q, kc, vc, ks, vs, gate, rows, history, round_q_half=0)
+    assert rel_l2(y, ref) <= REL_L2 and np.abs(y - ref).max() <= MAX_ABS, (rel_l2(y, ref), np.abs(y - ref).max())
+    cache.dispose()
+
+
 def test_decode_fused_vs_reference_reader(device, oracle):
     """The fused decode and the engine's scalar reader agree (Int8KvTests.cs:159-170 bound)."""
     history, rows = 4093, 7
