@@ -17,6 +17,7 @@
 //     and probabilities as the reference does (score = dot * ks[t] / 16,
 //     P = p * vs[t]).
 #include "common.h"
+#include <type_traits>
 #include "mfma.h"
 
 namespace boot {
@@ -167,13 +168,17 @@ __device__ inline void add_row_partner8(floatx4 &a, floatx4 &b) {
     b = floatx4{r4, r5, r6, r7};
 }
 
-// One chunk of one KV group in flight: thread t holds K rows t / 16 + 32 i (16 bytes
-// at 16 (t % 16)) and V page-row segments t / 8 + 64 i (16 bytes at 16 (t % 8)),
-// i < 4: every load instruction reads whole 256-byte K rows or whole 128-byte V
-// lines, the pattern that streams at full HBM rate (loads shaped like the MFMA
-// operands, 16 rows per instruction, reach about two thirds of it).
-struct ChunkRegs {
-    uint4 k0, k1, k2, k3, v0, v1, v2, v3;   // named, not an array: kept in registers
+// One chunk of one KV group in flight, K and V in separate register sets (K is staged
+// one chunk ahead of V): thread t holds K rows t / 16 + 32 i (16 bytes at 16 (t % 16))
+// and V page-row segments t / 8 + 64 i (16 bytes at 16 (t % 8)), i < 4: every load
+// instruction reads whole 256-byte K rows or whole 128-byte V lines, the pattern that
+// streams at full HBM rate (loads shaped like the MFMA operands, 16 rows per
+// instruction, reach about two thirds of it).
+struct KRegs {
+    uint4 k0, k1, k2, k3;   // named, not an array: kept in registers
+};
+struct VRegs {
+    uint4 v0, v1, v2, v3;
 };
 
 // The LDS image of a chunk. K: 128 token rows of 256 bytes, 16-byte piece c of
@@ -191,13 +196,19 @@ __device__ __attribute__((always_inline)) inline uint4 load_k_piece(const Decode
     return *reinterpret_cast<const uint4 *>(p.k + ((size_t)t * 2 + g) * 256 + 16 * (tid & 15));
 }
 
-// Chunk idx of the split starting at token `begin`. Past the last chunk (only the
-// prologue's loads of a split shorter than three chunks) the loads stay, a fixed
-// count that keeps the counter waits exact, but every lane reads the same 16 bytes
-// of the first one: a cache line instead of a 64 KB re-read.
-__device__ __attribute__((always_inline)) inline void load_chunk(ChunkRegs &r, const DecodeParams &p, uint32_t g,
-                                                                 uint32_t begin, uint32_t idx, uint32_t nchunks,
-                                                                 uint32_t length, int tid) {
+// 16 bytes as a value (a struct copy straight from global memory would keep the
+// register set in a stack object)
+__device__ __attribute__((always_inline)) inline uint4 load_piece(const int8_t *at) {
+    return *reinterpret_cast<const uint4 *>(at);
+}
+
+// K or V of chunk idx of the split starting at token `begin`. Past the last chunk
+// (only the prologue's loads of a split shorter than three chunks) the loads stay, a
+// fixed count that keeps the counter waits exact, but every lane reads the same 16
+// bytes of the first one: a cache line instead of a 32 KB re-read.
+__device__ __attribute__((always_inline)) inline void load_k(KRegs &r, const DecodeParams &p, uint32_t g,
+                                                             uint32_t begin, uint32_t idx, uint32_t nchunks,
+                                                             uint32_t length, int tid) {
     const bool real = idx < nchunks;
     const uint32_t c0 = real ? begin + idx * kChunk : begin;
     const int lt = real ? tid : 0;
@@ -205,22 +216,33 @@ __device__ __attribute__((always_inline)) inline void load_chunk(ChunkRegs &r, c
     r.k1 = load_k_piece(p, g, c0, length, lt, real ? 1 : 0);
     r.k2 = load_k_piece(p, g, c0, length, lt, real ? 2 : 0);
     r.k3 = load_k_piece(p, g, c0, length, lt, real ? 3 : 0);
+}
+
+__device__ __attribute__((always_inline)) inline void load_v(VRegs &r, const DecodeParams &p, uint32_t g,
+                                                             uint32_t begin, uint32_t idx, uint32_t nchunks,
+                                                             int tid) {
+    const bool real = idx < nchunks;
+    const uint32_t c0 = real ? begin + idx * kChunk : begin;
+    const int lt = real ? tid : 0;
     // c0 is a multiple of 128 inside the cache's whole pages
     const int8_t *vrow = p.v + value_index((uint64_t)c0 * 2 + g, 0) + (size_t)(lt >> 3) * 256 + 16 * (lt & 7);
     const size_t step = real ? 64 * 256 : 0;
-    r.v0 = *reinterpret_cast<const uint4 *>(vrow);
-    r.v1 = *reinterpret_cast<const uint4 *>(vrow + step);
-    r.v2 = *reinterpret_cast<const uint4 *>(vrow + 2 * step);
-    r.v3 = *reinterpret_cast<const uint4 *>(vrow + 3 * step);
+    r.v0 = load_piece(vrow);
+    r.v1 = load_piece(vrow + step);
+    r.v2 = load_piece(vrow + 2 * step);
+    r.v3 = load_piece(vrow + 3 * step);
 }
 
-__device__ __attribute__((always_inline)) inline void store_chunk(ChunkLds &b, const ChunkRegs &r, int tid) {
+__device__ __attribute__((always_inline)) inline void store_k(ChunkLds &b, const KRegs &r, int tid) {
     const int t = tid >> 4, c = tid & 15;   // K rows t + 32i (t + 32i has the same t % 16)
     const int kp = c ^ (t & 15);
     b.k[t][kp] = r.k0;
     b.k[t + 32][kp] = r.k1;
     b.k[t + 64][kp] = r.k2;
     b.k[t + 96][kp] = r.k3;
+}
+
+__device__ __attribute__((always_inline)) inline void store_v(ChunkLds &b, const VRegs &r, int tid) {
     const int d = tid >> 3, e = tid & 7;    // V rows d + 64i (same (d / 2) % 8)
     const int vp = e ^ ((d >> 1) & 7);
     b.v[d][vp] = r.v0;
@@ -247,8 +269,8 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
     // the chunk buffers
     __shared__ __attribute__((aligned(16))) unsigned char arena[2 * sizeof(ChunkLds)];
     ChunkLds *bufs = reinterpret_cast<ChunkLds *>(arena);
-    __shared__ float chunk_top[kDecodeWaves][16], wave_l[kDecodeWaves][16];
-    __shared__ uint2 pshare[kDecodeWaves][64];   // each wave's P operand of the chunk
+    __shared__ float chunk_top[2][kDecodeWaves][16], wave_l[kDecodeWaves][16];
+    __shared__ uint2 pshare[2][kDecodeWaves][64];   // each wave's P operands, by chunk parity
     __shared__ float kscale[kMaxSplitTokens], vscale[kMaxSplitTokens];
     __shared__ float red[kDecodeWaves], qmax[4][8];
     __shared__ v4i qlds[4][64];    // INT8 query operands, [MFMA c][lane]
@@ -288,9 +310,12 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    ChunkRegs r1, r2;
-    load_chunk(r2, p, g, begin, 0, nchunks, length, tid);
-    load_chunk(r1, p, g, begin, 1, nchunks, length, tid);
+    KRegs ka, kb;   // K of even / odd chunks
+    VRegs va, vb;   // V of even / odd chunks
+    load_k(ka, p, g, begin, 0, nchunks, length, tid);
+    load_v(va, p, g, begin, 0, nchunks, tid);
+    load_k(kb, p, g, begin, 1, nchunks, length, tid);
+    load_v(vb, p, g, begin, 1, nchunks, tid);
 
     // ---- scales of the split (this group) into LDS, vs_ref = their maximum; the
     // per-head maxima of the query chunks
@@ -334,10 +359,9 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
         for (int f = 0; f < 4; f++) w[f] = part(x[f].x) | (part(x[f].y) << 8) | (part(x[f].z) << 16) | (part(x[f].w) << 24);
         if (wave < 4) qlds[wave][lane] = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
     }
-    // chunk 0 into buffer 0 and chunk 2 into the registers it leaves: the loop
-    // below starts with r1 = chunk 1, r2 = chunk 2
-    store_chunk(bufs[0], r2, tid);
-    load_chunk(r2, p, g, begin, 2, nchunks, length, tid);
+    // K of chunk 0 into buffer 0 and K of chunk 2 into the registers it leaves
+    store_k(bufs[0], ka, tid);
+    load_k(ka, p, g, begin, 2, nchunks, length, tid);
     __syncthreads();
     v4i qi[4];
 #pragma unroll
@@ -348,120 +372,137 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
     o[1] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     float m = -INFINITY, l = 0.0f;
 
-    // one chunk from LDS: QK, the online softmax, PV
-    auto compute = [&](const ChunkLds &b, uint32_t c) {
-        const int tl = 16 * wave + (lane & 15);          // the lane's K row of the chunk
-        // S^T: rows = tokens 16w + 4qq + r of the chunk, columns n
-        v4i acc = {0, 0, 0, 0};
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, b.k[tl][(4 * j + qq) ^ (tl & 15)]), qi[j], acc, 0, 0, 0);
-        // the partner column n ^ 8 holds the other part of the same head
-        const int local0 = (int)(c * kChunk) + 16 * wave + 4 * qq;   // token offset inside the split
-        const uint32_t t0 = begin + (uint32_t)local0;
-        float sc[4];
-        float top = -INFINITY;
+    // Probabilities of the lane's four tokens against reference ref, as the FP16 hi (column
+    // n < 8) or lo (n >= 8) part of p * vs / vs_ref, published as this wave's P operand in
+    // slot `slot`; total = the column's sum over the wave's 16 tokens.
+    auto probs = [&](const float (&sc)[4], int local0, float ref, float &total, int slot) __attribute__((always_inline)) {
+        _Float16 hv[4];
+        total = 0.0f;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const int mine = acc[r], other = __shfl_xor(mine, 8, 64);
-            const float full = ((float)(lo_col ? other : mine) + (float)(lo_col ? mine : other) * (1.0f / 254.0f)) * qsc;
-            const float value = t0 + r < end ? full * kscale[local0 + r] : -INFINITY;
-            sc[r] = value;
-            top = fmaxf(top, value);
+            const float prob = ref == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc[r] - ref);   // 0 for masked tokens
+            total += prob;
+            const float scaled = prob * (vscale[local0 + r] * vs_inv);
+            const _Float16 hi = (_Float16)scaled;
+            hv[r] = lo_col ? (_Float16)(scaled - (float)hi) : hi;
         }
-        top = fmaxf(top, __shfl_xor(top, 16, 64));
-        top = fmaxf(top, __shfl_xor(top, 32, 64));
-        // the waves share one running reference m per column; a chunk rescales (and pays a
-        // second barrier) only when some column's maximum passes m by more than 2^8, so
-        // p = 2^(s - m) stays below 256
-        auto probs = [&](float ref, float &total) {
-            _Float16 hv[4];
-            total = 0.0f;
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const float prob = ref == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc[r] - ref);   // 0 for masked tokens
-                total += prob;
-                const float scaled = prob * (vscale[local0 + r] * vs_inv);
-                const _Float16 hi = (_Float16)scaled;
-                hv[r] = lo_col ? (_Float16)(scaled - (float)hi) : hi;
-            }
-            total += __shfl_xor(total, 16, 64);
-            total += __shfl_xor(total, 32, 64);
-            const half4 pop = {hv[0], hv[1], hv[2], hv[3]};
-            pshare[wave][lane] = __builtin_bit_cast(uint2, pop);
-        };
-        float total;
-        probs(m, total);
-        if (qq == 0) chunk_top[wave][n] = top;
-        __syncthreads();
-        float ctop = chunk_top[0][n];
-#pragma unroll
-        for (int w = 1; w < kDecodeWaves; w++) ctop = fmaxf(ctop, chunk_top[w][n]);
-        // every wave reads the same maxima: the branch is uniform over the work-group
-        if (__builtin_amdgcn_ballot_w64(ctop > m + 8.0f) != 0) {
-            const float next = fmaxf(m, ctop);
-            const float decay = next == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - next);
-            l *= decay;
-            o[0] *= decay;
-            o[1] *= decay;
-            m = next;
-            probs(m, total);   // no wave reads P before this branch
-            __syncthreads();
-        }
-        l += total;   // this wave's tokens
-        // O^T[d][n] += V^T[d][t] P[t][n] for this wave's 32 dimensions over the chunk's 128
-        // tokens: k-step src takes wave src's tokens 16 src..16 src+15 and P operand
-#pragma unroll
-        for (int src = 0; src < kDecodeWaves; src++) {
-            const half4 ps = __builtin_bit_cast(half4, pshare[src][lane]);
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const int d = 16 * (2 * wave + j) + n;
-                const uint32_t w4 = reinterpret_cast<const uint32_t *>(&b.v[d][src ^ ((d >> 1) & 7)])[qq];
-                uint32_t h0, h1;
-                i8x4_to_f16(w4, h0, h1);
-                const half4 va = __builtin_bit_cast(half4, make_uint2(h0, h1));
-                o[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, ps, o[j], 0, 0, 0);
-            }
-        }
+        total += __shfl_xor(total, 16, 64);
+        total += __shfl_xor(total, 32, 64);
+        const half4 pop = {hv[0], hv[1], hv[2], hv[3]};
+        pshare[slot][wave][lane] = __builtin_bit_cast(uint2, pop);
     };
-    // Chunks in pairs, so that the two register sets take turns without copies (a
-    // copy of registers still being loaded waits for the load). At the top of a
-    // pair: buffer 0 holds chunk c, r1 chunk c + 1, r2 chunk c + 2. The pairs run
-    // while every load is a real chunk (a fixed count per pair keeps the counter
-    // waits exact); the last one to four chunks follow without loads past the end,
-    // whose registers the merge below would otherwise wait for. (A third register
-    // set, three chunks in flight, measured slower: the longer start-up burst delays
-    // every work-group's first chunk.)
-    uint32_t c = 0;
-    for (; c + 4 < nchunks; c += 2) {
-        compute(bufs[0], c);
-        store_chunk(bufs[1], r1, tid);   // buffer 1's chunk c - 1 was finished before the last barrier
-        load_chunk(r1, p, g, begin, c + 3, nchunks, length, tid);
-        __syncthreads();
-        compute(bufs[1], c + 1);
-        store_chunk(bufs[0], r2, tid);
-        load_chunk(r2, p, g, begin, c + 4, nchunks, length, tid);
-        __syncthreads();
-    }
-    if (c < nchunks) {
-        compute(bufs[0], c);
-        if (c + 1 < nchunks) {
-            store_chunk(bufs[1], r1, tid);
-            if (c + 3 < nchunks) load_chunk(r1, p, g, begin, c + 3, nchunks, length, tid);
-            __syncthreads();
-            compute(bufs[1], c + 1);
-            if (c + 2 < nchunks) {
-                store_chunk(bufs[0], r2, tid);
+    // the previous chunk's scores, kept for a rebuild of its operands
+    float sc_prev[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    float total_prev = 0.0f;
+    int local_prev = 0;
+    // Phase j (one barrier each): finish chunk j - 1 (the rescale decision, then PV), score
+    // chunk j, store V of chunk j and K of chunk j + 1, load V of chunk j + 2 and K of chunk
+    // j + 3 into the registers just stored. K is staged one chunk ahead of V, so the two
+    // buffers' K and V halves have different lifetimes: in phase j chunk j - 1's V and chunk
+    // j's K are read while chunk j's V and chunk j + 1's K are written.
+    // The waves share one running reference m per column; a chunk rescales (and pays a
+    // second barrier) only when some column's maximum passes m by more than 2^8, so
+    // p = 2^(s - m) stays below 256.
+    auto finish = [&](uint32_t j) __attribute__((always_inline)) {   // chunk j - 1, j > 0
+        {
+            const int slot = (j - 1) & 1;
+            float ctop = chunk_top[slot][0][n];
+#pragma unroll
+            for (int w = 1; w < kDecodeWaves; w++) ctop = fmaxf(ctop, chunk_top[slot][w][n]);
+            // every wave reads the same maxima: the branch is uniform over the work-group
+            if (__builtin_amdgcn_ballot_w64(ctop > m + 8.0f) != 0) {
+                const float next = fmaxf(m, ctop);
+                const float decay = next == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - next);
+                l *= decay;
+                o[0] *= decay;
+                o[1] *= decay;
+                m = next;
+                probs(sc_prev, local_prev, m, total_prev, slot);   // no wave reads the slot before this branch
                 __syncthreads();
-                compute(bufs[0], c + 2);
-                if (c + 3 < nchunks) {
-                    store_chunk(bufs[1], r1, tid);
-                    __syncthreads();
-                    compute(bufs[1], c + 3);
+            }
+            l += total_prev;   // this wave's tokens
+            // O^T[d][n] += V^T[d][t] P[t][n] for this wave's 32 dimensions over the chunk's 128
+            // tokens: k-step src takes wave src's tokens 16 src..16 src+15 and P operand
+            const ChunkLds &b = bufs[slot];
+#pragma unroll
+            for (int src = 0; src < kDecodeWaves; src++) {
+                const half4 ps = __builtin_bit_cast(half4, pshare[slot][src][lane]);
+#pragma unroll
+                for (int jj = 0; jj < 2; jj++) {
+                    const int d = 16 * (2 * wave + jj) + n;
+                    const uint32_t w4 = reinterpret_cast<const uint32_t *>(&b.v[d][src ^ ((d >> 1) & 7)])[qq];
+                    uint32_t h0, h1;
+                    i8x4_to_f16(w4, h0, h1);
+                    const half4 va4 = __builtin_bit_cast(half4, make_uint2(h0, h1));
+                    o[jj] = __builtin_amdgcn_mfma_f32_16x16x16f16(va4, ps, o[jj], 0, 0, 0);
                 }
             }
         }
+    };
+    // odd: a compile-time parity of j, which picks the register sets (V of chunk j, K of
+    // chunk j + 1) without taking their addresses
+    auto phase = [&](uint32_t j, auto odd, bool store_knext, bool load_v2, bool load_k3) __attribute__((always_inline)) {
+        VRegs &rv = decltype(odd)::value ? vb : va;
+        KRegs &rk = decltype(odd)::value ? ka : kb;
+        if (j > 0) finish(j);
+        {
+            const ChunkLds &b = bufs[j & 1];
+            const int tl = 16 * wave + (lane & 15);          // the lane's K row of the chunk
+            // S^T: rows = tokens 16w + 4qq + r of the chunk, columns n
+            v4i acc = {0, 0, 0, 0};
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++)
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, b.k[tl][(4 * jj + qq) ^ (tl & 15)]), qi[jj], acc, 0, 0, 0);
+            // the partner column n ^ 8 holds the other part of the same head
+            const int local0 = (int)(j * kChunk) + 16 * wave + 4 * qq;   // token offset inside the split
+            const uint32_t t0 = begin + (uint32_t)local0;
+            float top = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int mine = acc[r], other = __shfl_xor(mine, 8, 64);
+                const float full = ((float)(lo_col ? other : mine) + (float)(lo_col ? mine : other) * (1.0f / 254.0f)) * qsc;
+                const float value = t0 + r < end ? full * kscale[local0 + r] : -INFINITY;
+                sc_prev[r] = value;
+                top = fmaxf(top, value);
+            }
+            top = fmaxf(top, __shfl_xor(top, 16, 64));
+            top = fmaxf(top, __shfl_xor(top, 32, 64));
+            local_prev = local0;
+            probs(sc_prev, local0, m, total_prev, j & 1);
+            if (qq == 0) chunk_top[j & 1][wave][n] = top;
+        }
+        store_v(bufs[j & 1], rv, tid);
+        if (load_v2) load_v(rv, p, g, begin, j + 2, nchunks, tid);
+        if (store_knext) store_k(bufs[(j + 1) & 1], rk, tid);
+        if (load_k3) load_k(rk, p, g, begin, j + 3, nchunks, length, tid);
+        __syncthreads();
+    };
+    // Phases in pairs, so that the register sets keep fixed roles without copies (a copy of
+    // registers still being loaded waits for the load). The pairs run while every load is
+    // a real chunk (a fixed count per pair keeps the counter waits exact); the last one to
+    // four chunks follow without loads past the end, whose registers the end of the
+    // work-group would otherwise wait for.
+    uint32_t c = 0;
+    for (; c + 4 < nchunks; c += 2) {
+        phase(c, std::false_type{}, true, true, true);
+        phase(c + 1, std::true_type{}, true, true, true);
+    }
+    if (c < nchunks) {
+        phase(c, std::false_type{}, c + 1 < nchunks, c + 2 < nchunks, c + 3 < nchunks);
+        uint32_t last_phase = c + 1;
+        if (c + 1 < nchunks) {
+            phase(c + 1, std::true_type{}, c + 2 < nchunks, c + 3 < nchunks, false);
+            last_phase = c + 2;
+            if (c + 2 < nchunks) {
+                phase(c + 2, std::false_type{}, c + 3 < nchunks, false, false);
+                last_phase = c + 3;
+                if (c + 3 < nchunks) {
+                    phase(c + 3, std::true_type{}, false, false, false);
+                    last_phase = c + 4;
+                }
+            }
+        }
+        finish(last_phase);
     }
 
     // ---- the waves share m; l sums over waves. O^T[d][n], d = 16 dt + 4 qq + r: the lo
