@@ -89,11 +89,14 @@ __device__ inline float4 rope4(float4 x, int lane, const Rope4 &r) {
     return make_float4(out[0], out[1], out[2], out[3]);
 }
 
-// pow(theta, -float(2*j)/64.0f) in fp32 for lane j < 32 (kernels.metal:123), computed
-// per wave in registers: no LDS table and no barrier, so a kernel's loads go out first.
+// pow(theta, -float(2*j)/64.0f) as an fp32 value for lane j < 32 (kernels.metal:123):
+// evaluated in fp64 and rounded once, so it is the correctly rounded fp32 value of the
+// reference's expression (theta and the exponent are exact in fp32). One ulp of it moves
+// the angle at position 262143 by ~0.016 rad. Computed per wave in registers: no LDS
+// table and no barrier, so a kernel's loads go out first.
 __device__ inline float lane_inv_freq(float theta) {
     const int j = threadIdx.x & 63;
-    return j < 32 ? powf(theta, -(float)(2 * j) / 64.0f) : 0.0f;
+    return j < 32 ? (float)pow((double)theta, (double)(-(float)(2 * j) / 64.0f)) : 0.0f;
 }
 
 // RMS normalization of one 256-dim vector held as a float4 per lane, with the

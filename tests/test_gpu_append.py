@@ -81,6 +81,54 @@ def test_heavy_tailed_outliers_bitexact(device, oracle):
     assert_same_bytes(*run_store(device, oracle, k, v, 131072 - 512, guard=0))
 
 
+def rotate_fp32_angle(x, position, theta=1e7):
+    """kernels.metal:122-125 with the reference's FP32 angle: angle = float(position) *
+    float(theta^(-2j/64)) rounded to FP32 at each step, then an exact rotation of that angle
+    (FP64 cos/sin); dims >= 64 pass through."""
+    x = np.asarray(x, np.float64)
+    j = np.arange(32)
+    ifreq = np.power(np.float64(theta), -2.0 * j / 64.0).astype(np.float32)
+    angle = (np.float32(position) * ifreq).astype(np.float32).astype(np.float64)
+    out = x.copy()
+    a, b = x[:32], x[32:64]
+    out[:32] = a * np.cos(angle) - b * np.sin(angle)
+    out[32:64] = b * np.cos(angle) + a * np.sin(angle)
+    return out
+
+
+def test_batch_rope_int8_fp32_angles_deep_window(device, oracle):
+    """The last 8 positions of the 262144-token window, where an FP32 angle is off from the exact
+    one by up to ~0.016 rad: the rotation must follow the reference's FP32 angle arithmetic
+    (kernels.metal:122-125), so against that restatement the error is the FP32 rounding of
+    cos/sin and of the rotation alone."""
+    rows, position = 8, 262136
+    length = position + rows
+    q = oracle.fill_hash(rows * 4096, 41, 3)
+    k = oracle.fill_hash(rows * 512, 43, 3)
+    v = oracle.fill_hash(rows * 512, 47, 1)
+    kc, vc, ks, vs = oracle.empty_cache(length)
+    bufs = [upload(device, a) for a in (kc, vc, ks, vs)]
+    qb, kb, vb = upload(device, q), upload(device, k), upload(device, v)
+    qr = device.allocate(q.nbytes)
+    layer = engine.Int8KvLayer.__new__(engine.Int8KvLayer)
+    layer.key, layer.value, layer.key_scale, layer.value_scale = bufs
+    device.begin()
+    engine.append_rows(device, layer, qb, kb, vb, qr, rows, position)
+    device.end()
+    rotated_q = qr.read(np.float32, rows * 4096)
+    exact_gap = 0.0
+    for row in range(rows):
+        for head in range(16):
+            src = q[(row * 16 + head) * 256:][:256]
+            ref = rotate_fp32_angle(src, position + row)
+            got = rotated_q[(row * 16 + head) * 256:][:256]
+            assert np.max(np.abs(got - ref)) < 2e-5, (row, head, np.max(np.abs(got - ref)))
+            exact_gap = max(exact_gap, np.max(np.abs(ref - oracle.rotate_vector_f64(src, position + row))))
+    assert exact_gap > 1e-3          # the FP32 angle is far from the exact one this deep
+    for b in bufs + [qb, kb, vb, qr]:
+        b.dispose()
+
+
 def test_batch_rope_int8(device, oracle):
     """Int8KvTests.Store (Int8KvTests.cs:33-70) with its inputs and bounds: position 4093,
     33 rows, zero vectors, outliers; Q rotation against FP64 (KvStorageTests.cs:55)."""
