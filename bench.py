@@ -252,7 +252,8 @@ def main():
                          "reference that scales rocprofv3 FETCH_SIZE / WRITE_SIZE into bytes")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is design-only (DESIGN.md)",
+        print(json.dumps({"error": "this build runs on one GPU; sharding the KV path across GPUs (by KV head, "
+                                   "layer or sequence range) is a design, not built",
                           "n_gpus": args.gpus}))
         sys.exit(2)
 
