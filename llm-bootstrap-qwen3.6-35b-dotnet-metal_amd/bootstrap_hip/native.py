@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import weakref
 from typing import NamedTuple, Optional
 
 import numpy as np
@@ -123,9 +124,12 @@ class GpuBuffer:
         return Binding(self, offset)
 
     def dispose(self) -> None:
-        if self.handle:
+        """Releases the buffer once. After ``Device.close`` the context has already freed
+        every buffer it owned (boot_destroy), so the handle is then only forgotten."""
+        if self.handle and self.device.handle:
             self.device.lib.boot_release_buffer(self.handle)
-            self.handle = 0
+            self.device._live.discard(self)
+        self.handle = 0
 
     def __enter__(self):
         return self
@@ -143,6 +147,7 @@ class Device:
         if not handle:
             raise HipError("HIP device unavailable or not gfx950 (boot_create returned NULL)")
         self.handle = handle
+        self._live = weakref.WeakSet()   # buffers whose handles close() must invalidate
 
     # Metal.cs:69
     def _check(self, result: int) -> None:
@@ -159,7 +164,9 @@ class Device:
         handle = self.lib.boot_buffer(self.handle, nbytes)
         if not handle:
             self._check(0)
-        return GpuBuffer(self, handle, nbytes)
+        buffer = GpuBuffer(self, handle, nbytes)
+        self._live.add(buffer)
+        return buffer
 
     def set_profiling(self, enabled: bool) -> None:
         self.lib.boot_profile(self.handle, 1 if enabled else 0)
@@ -217,7 +224,12 @@ class Device:
                                            threads_x, threads_y, 1, group, 1, 1, None, 0))
 
     def close(self) -> None:
+        """Metal.cs:114. boot_destroy frees the context and every buffer it still owns, so the
+        handles of live GpuBuffer objects are invalidated here (a later dispose is a no-op)."""
         if self.handle:
+            for buffer in list(self._live):
+                buffer.handle = 0
+            self._live.clear()
             self.lib.boot_destroy(self.handle)
             self.handle = 0
 

@@ -243,6 +243,142 @@ void kvref_attention_fp16kv_f64(const float *q, int round_q_half,
     run_attention(&j, threads);
 }
 
+/* ---------------------------------------------------------------- online emulator */
+
+typedef struct {
+    const float *q;
+    const int8_t *kc, *vc;
+    const float *ks, *vs, *gate;
+    int rows, pos, tile_keys, p_mode;
+    float *out;
+    int64_t next, total;
+    pthread_mutex_t lock;
+} online_job;
+
+static float sigmoid_f32(float g) {
+    volatile float e = expf(-g);
+    volatile float d = 1.0f + e;
+    return 1.0f / d;
+}
+
+/* One (row, head) of the reference's tuned online INT8 prefill, kernels.metal:1378-1457,
+ * with its roundings: FP16 query (:1276-1281); per 256-key tile the FP32 score
+ * (q16 . code) scaled as (s * (1/16)) * ks (:1419-1421), masked beyond pos + row; the tile
+ * maximum joins the running one (:1424), decay = exp(old - new) and the unscaled exponentials
+ * exp(a - new) in FP32 (:1425-1426); the probability operand P = bfloat(e * vs) (:1427);
+ * the denominator sums the unrounded e (:1428-1429); the accumulator is scaled by the decay
+ * (:1436-1437) and gains sum_t P_t * vcode_t (BF16 x INT8 products are exact; the tile's sum
+ * is rounded to FP32 once, :1438-1447); y = out / denominator * sigmoid(gate) (:1452-1453).
+ * The FP32 dot products and tile sums are formed in FP64 and rounded once (the matrix units'
+ * summation order is not observable here); exp is the C library's expf.
+ * p_mode 1 replaces (:1427) by this build's rounding, FP16(e * (vs / vs_ref)) with vs_ref the
+ * largest V scale over the attended keys, and multiplies vs_ref back at the end;
+ * p_mode 2 keeps P = e * vs in FP32 (no operand rounding). */
+static void online_one(online_job *j, int row, int head, float *vals) {
+    const int g = head / 8, length = j->pos + row + 1, T = j->tile_keys;
+    float q[256];
+    for (int d = 0; d < 256; d++)
+        q[d] = kvref_half_to_float(kvref_half_bits(j->q[((size_t)row * 16 + head) * 256 + d]));
+    float vs_ref = 0.0f;
+    for (int t = 0; t < length; t++) {
+        float v = j->vs[(size_t)t * 2 + g];
+        if (v > vs_ref) vs_ref = v;
+    }
+    volatile float vs_inv = vs_ref > 0.0f ? 1.0f / vs_ref : 0.0f;
+    float out[256];
+    for (int d = 0; d < 256; d++) out[d] = 0.0f;
+    float maximum = -INFINITY, denominator = 0.0f;
+    for (int key = 0; key < length; key += T) {
+        int n = length - key < T ? length - key : T;
+        float top = -INFINITY;
+        for (int i = 0; i < n; i++) {
+            int t = key + i;
+            const int8_t *k = j->kc + ((size_t)t * 2 + g) * 256;
+            double dot = 0;
+            for (int d = 0; d < 256; d++) dot += (double)q[d] * (double)k[d];
+            volatile float s = (float)dot;
+            volatile float a = s * (1.0f / 16.0f);
+            volatile float b = a * j->ks[(size_t)t * 2 + g];
+            vals[i] = b;
+            if (b > top) top = b;
+        }
+        float next = maximum > top ? maximum : top;
+        volatile float decay = expf(maximum - next);
+        float total = 0.0f;
+        double tile[256];
+        for (int d = 0; d < 256; d++) tile[d] = 0;
+        for (int i = 0; i < n; i++) {
+            int t = key + i;
+            volatile float value = expf(vals[i] - next);
+            float vsc = j->vs[(size_t)t * 2 + g];
+            float p;
+            if (j->p_mode == 0) {
+                volatile float scaled = value * vsc;
+                p = kvref_bf16_round(scaled);
+            } else if (j->p_mode == 1) {
+                volatile float ratio = vsc * vs_inv;
+                volatile float scaled = value * ratio;
+                p = kvref_half_to_float(kvref_half_bits(scaled));
+            } else {
+                volatile float scaled = value * vsc;
+                p = scaled;
+            }
+            total += value;
+            uint64_t page = kvref_value_index((uint32_t)t * 2u + (uint32_t)g, 0);
+            for (int d = 0; d < 256; d++) tile[d] += (double)p * (double)j->vc[page + (uint64_t)d * 256u];
+        }
+        volatile float scaled_denominator = denominator * decay;
+        denominator = scaled_denominator + total;
+        maximum = next;
+        for (int d = 0; d < 256; d++) {
+            volatile float kept = out[d] * decay;
+            volatile float gained = (float)tile[d];
+            out[d] = kept + gained;
+        }
+    }
+    float *y = j->out + ((size_t)row * 16 + head) * 256;
+    for (int d = 0; d < 256; d++) {
+        volatile float o = j->p_mode == 1 ? out[d] * vs_ref : out[d];
+        volatile float r = o / denominator;
+        y[d] = r * sigmoid_f32(j->gate[((size_t)row * 16 + head) * 256 + d]);
+    }
+}
+
+static void *online_worker(void *arg) {
+    online_job *j = (online_job *)arg;
+    float *vals = (float *)malloc(sizeof(float) * (size_t)j->tile_keys);
+    for (;;) {
+        pthread_mutex_lock(&j->lock);
+        int64_t item = j->next++;
+        pthread_mutex_unlock(&j->lock);
+        if (item >= j->total) break;
+        online_one(j, (int)(item / 16), (int)(item % 16), vals);
+    }
+    free(vals);
+    return NULL;
+}
+
+void kvref_attention_online_emulate(const float *q, const int8_t *kc, const int8_t *vc,
+                                    const float *ks, const float *vs, const float *gate,
+                                    int rows, int pos, int tile_keys, int p_mode,
+                                    float *out, int threads) {
+    online_job j;
+    memset(&j, 0, sizeof j);
+    j.q = q; j.kc = kc; j.vc = vc; j.ks = ks; j.vs = vs; j.gate = gate;
+    j.rows = rows; j.pos = pos; j.tile_keys = tile_keys > 0 ? tile_keys : 256; j.p_mode = p_mode;
+    j.out = out; j.next = 0; j.total = (int64_t)rows * 16;
+    pthread_mutex_init(&j.lock, NULL);
+    if (threads < 1) threads = 1;
+    if (threads > 256) threads = 256;
+    pthread_t tid[256];
+    int started = 0;
+    for (int i = 1; i < threads; i++)
+        if (pthread_create(&tid[started], NULL, online_worker, &j) == 0) started++;
+    online_worker(&j);
+    for (int i = 0; i < started; i++) pthread_join(tid[i], NULL);
+    pthread_mutex_destroy(&j.lock);
+}
+
 /* ---------------------------------------------------------------- generators */
 
 void kvref_fill_hash(float *out, int64_t count, uint32_t seed, float scale) {

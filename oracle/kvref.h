@@ -23,6 +23,16 @@
  *   kvref_attention_f64    brute force vs an independent NumPy float64 softmax on
  *                          small shapes; one key -> v*sigmoid(g); equal scores ->
  *                          mean of v; equal queries -> equal outputs across heads
+ *   kvref_attention_fp16kv_f64  an independent NumPy float64 softmax over FP16-decoded K/V
+ *                          on small shapes; one key -> v*sigmoid(g); equal keys -> mean of
+ *                          v; equal queries -> equal outputs across the heads of a group
+ *   kvref_attention_online_emulate  p_mode 2 (no operand rounding) equals
+ *                          kvref_attention_f64 to FP32 rounding, for 1-key and multi-tile
+ *                          histories (the tile recurrence: maxima, decays, denominators);
+ *                          one key -> exactly round(vs)*code*sigmoid(g) in each p_mode (the
+ *                          operand rounding and where vs_ref enters); the BF16 and FP16
+ *                          roundings themselves are pinned by NumPy/torch (kvref_half_bits,
+ *                          kvref_bf16_round)
  *   kvref_fill_hash        reproduces the integer hash generator; known values
  *                          computed from the formula in Python integers (tests)
  */
@@ -86,6 +96,18 @@ void kvref_attention_f64(const float *q, int round_q_half,
 void kvref_attention_fp16kv_f64(const float *q, int round_q_half,
                                 const uint16_t *kh, const uint16_t *vh, const float *gate,
                                 int rows, int pos, double *out, int threads);
+
+/* The reference's tuned online INT8 prefill (kernels.metal:1378-1457) evaluated with its
+ * roundings, one (row, head) at a time: FP16 Q, FP32 scores scaled by (1/16) and ks, 256-key
+ * tiles (`tile_keys`) with a running FP32 maximum and denominator, probability operands
+ * P = bfloat(e * vs) against BF16 x INT8 products, FP32 output. p_mode 0: that BF16 operand
+ * (the reference); 1: FP16(e * vs / vs_ref), vs_ref = the largest V scale of the attended
+ * keys, multiplied back at the end (this build's kernels); 2: no operand rounding. FP32 out
+ * [rows][16][256]. Used to show what the operand rounding alone costs against FP64. */
+void kvref_attention_online_emulate(const float *q, const int8_t *kc, const int8_t *vc,
+                                    const float *ks, const float *vs, const float *gate,
+                                    int rows, int pos, int tile_keys, int p_mode,
+                                    float *out, int threads);
 
 /* Deterministic integer-hash fill. FastAttentionTests.cs:111-119 (Fill). */
 void kvref_fill_hash(float *out, int64_t count, uint32_t seed, float scale);

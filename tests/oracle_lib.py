@@ -45,6 +45,8 @@ class Oracle:
                                             ctypes.c_int, ctypes.c_int, _f64p, ctypes.c_void_p, ctypes.c_int]
         lib.kvref_attention_fp16kv_f64.argtypes = [_f32p, ctypes.c_int, _u16p, _u16p, _f32p,
                                                    ctypes.c_int, ctypes.c_int, _f64p, ctypes.c_int]
+        lib.kvref_attention_online_emulate.argtypes = [_f32p, _i8p, _i8p, _f32p, _f32p, _f32p, ctypes.c_int,
+                                                       ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p, ctypes.c_int]
         lib.kvref_fill_hash.argtypes = [_f32p, ctypes.c_int64, ctypes.c_uint32, ctypes.c_float]
         lib.kvref_normal.argtypes = [_f32p, ctypes.c_int64, ctypes.c_uint64]
         lib.kvref_splitmix64.argtypes = [ctypes.c_uint64, np.ctypeslib.ndpointer(np.uint64, flags="C_CONTIGUOUS"),
@@ -121,6 +123,15 @@ class Oracle:
         self.lib.kvref_attention_fp16kv_f64(np.ascontiguousarray(q, np.float32).ravel(), int(round_q_half),
                                             kh, vh, np.ascontiguousarray(gate, np.float32).ravel(),
                                             rows, pos, out, self.threads)
+        return out
+
+    def online_emulate(self, q, kc, vc, ks, vs, gate, rows, pos, p_mode, tile_keys=256):
+        """The reference's online INT8 prefill with its roundings; p_mode 0 BF16 operand
+        (kernels.metal:1427), 1 this build's FP16(e*vs/vs_ref), 2 unrounded."""
+        out = np.zeros(rows * 4096, np.float32)
+        self.lib.kvref_attention_online_emulate(np.ascontiguousarray(q, np.float32).ravel(), kc, vc, ks, vs,
+                                                np.ascontiguousarray(gate, np.float32).ravel(), rows, pos,
+                                                tile_keys, p_mode, out, self.threads)
         return out
 
     # ---- generators

@@ -84,3 +84,39 @@ def test_verify_slices_follow_the_workspace_budget():
         engine.verify_slices(8, 100, workspace_floats=16 * 100)               # not one row fits
     with pytest.raises(ValueError):
         engine.verify_slices(0, 100)
+
+
+class _RecordingLibrary:
+    """Stands in for libbootstrap_hip.so: hands out handles and records release/destroy calls."""
+
+    def __init__(self):
+        self.calls, self.next = [], 100
+
+    def boot_buffer(self, ctx, nbytes):
+        self.next += 1
+        return self.next
+
+    def boot_release_buffer(self, handle):
+        self.calls.append(("release", handle))
+
+    def boot_destroy(self, ctx):
+        self.calls.append(("destroy", ctx))
+
+    def boot_error(self, ctx):
+        return b"error"
+
+
+def test_buffer_dispose_after_device_close_does_not_release():
+    """boot_destroy frees every buffer the context owns (shim.cpp boot_destroy), so a buffer
+    disposed after Device.close must not reach boot_release_buffer (freed memory)."""
+    import weakref
+    from bootstrap_hip.native import Device
+    device = Device.__new__(Device)
+    device.lib, device.handle, device._live = _RecordingLibrary(), 7, weakref.WeakSet()
+    kept, released = device.allocate(64), device.allocate(64)
+    released.dispose()
+    released.dispose()                                   # a second dispose is a no-op
+    device.close()
+    kept.dispose()                                       # after close: handle forgotten only
+    assert device.lib.calls == [("release", 102), ("destroy", 7)]
+    assert kept.handle == 0 and released.handle == 0
