@@ -8,9 +8,10 @@
 //   * attention_decode_int8: one fused split-K pass that streams the INT8 K/V
 //     pages from HBM once, as whole K rows and whole 128-byte V page-row lines
 //     staged through LDS. Scores run on INT8 MFMA straight from the K codes:
-//     the FP32 query of each head is split into two INT8 parts,
-//     q ~= s_q (q1 + q2 / 254) with s_q = max|q| / 127 (error <= 1.55e-5 max|q|),
-//     which fill the 16 MFMA columns (8 heads x {q1, q2}). PV runs on FP16 MFMA
+//     the FP32 query of each head is split into three INT8 parts,
+//     q ~= s_q (q1 + q2 / 254 + q3 / 254^2) with s_q = max|q| / 127 (error
+//     <= 6.1e-8 max|q| per element, below the FP32 reader's own summation error),
+//     in two MFMAs whose 16 columns are 8 heads x {q1, q2} and 8 heads x q3. PV runs on FP16 MFMA
 //     with V codes dequantized exactly in registers and the scaled
 //     probabilities p*vs[t]/vs_ref (vs_ref = the largest V scale of the split, so
 //     they lie in [0, 1]) split into FP16 hi + lo. Scales are applied to scores
@@ -256,7 +257,7 @@ __device__ __attribute__((always_inline)) inline void store_v(ChunkLds &b, const
 // CUs in one round. The work-group streams its chunks through double-buffered LDS
 // with two chunks in flight in registers. Per chunk wave w scores tokens 16w..16w+15,
 // S^T[t][n] = K[t] . Qx[n] (16x16x64 INT8 MFMA on the raw K codes, n = 8 heads x
-// {q1, q2}), and turns them into probabilities in base 2 against a running reference
+// {q1, q2}, and a second product for q3), and turns them into probabilities in base 2 against a running reference
 // shared by the work-group; the waves exchange those P operands through LDS and wave w
 // accumulates O^T[d][n] += V^T[d][t] . Px[t][n] for dimensions 32w..32w+31 over all 128
 // tokens (16x16x16 FP16 MFMA), so no wave merge of O remains at the end. Px = p * vs /
@@ -273,7 +274,12 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
     __shared__ uint2 pshare[2][kDecodeWaves][64];   // each wave's P operands, by chunk parity
     __shared__ float kscale[kMaxSplitTokens], vscale[kMaxSplitTokens];
     __shared__ float red[kDecodeWaves], qmax[4][8];
-    __shared__ v4i qlds[4][64];    // INT8 query operands, [MFMA c][lane]
+    // INT8 query operands [set][MFMA c][lane] (set 0: q1 | q2 columns, set 1: q3), built once
+    // and read into registers before the chunk loop. They sit in the V half of chunk buffer
+    // 1, which is first written in phase 1, after the barrier that ends phase 0: by then every
+    // wave has read its operands.
+    v4i(*qlds)[4][64] = reinterpret_cast<v4i(*)[4][64]>(&bufs[1].v[0][0]);
+    static_assert(2 * 4 * 64 * sizeof(v4i) <= sizeof(ChunkLds::v), "query operands exceed the V half of a buffer");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = lane & 15, qq = lane >> 4, head = n & 7;
     const bool lo_col = n >= 8;
@@ -344,28 +350,45 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
 #pragma unroll
     for (int w = 1; w < kDecodeWaves; w++) vs_ref = fmaxf(vs_ref, red[w]);
     const float vs_inv = vs_ref > 0.0f ? 1.0f / vs_ref : 0.0f;
-    // ---- INT8 query operand of chunk c = wave: part n / 8 of q ~= s_q (q1 + q2 / 254)
+    // ---- INT8 query operands of chunk c = wave: q ~= s_q (q1 + q2 / 254 + q3 / 254^2).
+    // z = q / s_q lies in [-127, 127]; q1 = rint(z) and r1 = z - q1 (exact, |r1| <= 1/2);
+    // q2 = rint(254 r1) and r2 = 254 r1 - q2 (one rounding, |r2| <= 1/2 + 2^-17);
+    // q3 = rint(254 r2). Set 0 holds q1 in columns n < 8 and q2 in n >= 8, set 1 q3 in both.
     const float qabs = fmaxf(fmaxf(qmax[0][head], qmax[1][head]), fmaxf(qmax[2][head], qmax[3][head]));
     const float qsc = qabs * (1.0f / 127.0f);   // s_q of the lane's head
     {
         const float inv = qabs > 0.0f ? 127.0f / qabs : 0.0f;
-        auto part = [&](float v) {
-            const float z = v * inv, q1 = rintf(z);
-            const float q = lo_col ? rintf((z - q1) * 254.0f) : q1;
-            return (uint32_t)(uint8_t)(int8_t)(int)fminf(fmaxf(q, -127.0f), 127.0f);
-        };
-        uint32_t w[4];
+        auto code = [](float q) { return (uint32_t)(uint8_t)(int8_t)(int)fminf(fmaxf(q, -127.0f), 127.0f); };
+        uint32_t w[4], w3[4];
 #pragma unroll
-        for (int f = 0; f < 4; f++) w[f] = part(x[f].x) | (part(x[f].y) << 8) | (part(x[f].z) << 16) | (part(x[f].w) << 24);
-        if (wave < 4) qlds[wave][lane] = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+        for (int f = 0; f < 4; f++) {
+            const float xs[4] = {x[f].x, x[f].y, x[f].z, x[f].w};
+            w[f] = w3[f] = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float z = xs[e] * inv, q1 = rintf(z), r1 = z - q1;
+                const float q2 = rintf(r1 * 254.0f);
+                const float r2 = fmaf(r1, 254.0f, -q2);
+                const float q3 = rintf(r2 * 254.0f);
+                w[f] |= code(lo_col ? q2 : q1) << (8 * e);
+                w3[f] |= code(q3) << (8 * e);
+            }
+        }
+        if (wave < 4) {
+            qlds[0][wave][lane] = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+            qlds[1][wave][lane] = v4i{(int)w3[0], (int)w3[1], (int)w3[2], (int)w3[3]};
+        }
     }
     // K of chunk 0 into buffer 0 and K of chunk 2 into the registers it leaves
     store_k(bufs[0], ka, tid);
     load_k(ka, p, g, begin, 2, nchunks, length, tid);
     __syncthreads();
-    v4i qi[4];
+    v4i qi[4], q3i[4];
 #pragma unroll
-    for (int c = 0; c < 4; c++) qi[c] = qlds[c][lane];
+    for (int c = 0; c < 4; c++) {
+        qi[c] = qlds[0][c][lane];
+        q3i[c] = qlds[1][c][lane];
+    }
 
     floatx4 o[2];   // O^T tiles dt = 2 wave + i, over every token of the split
     o[0] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -448,19 +471,24 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
         {
             const ChunkLds &b = bufs[j & 1];
             const int tl = 16 * wave + (lane & 15);          // the lane's K row of the chunk
-            // S^T: rows = tokens 16w + 4qq + r of the chunk, columns n
-            v4i acc = {0, 0, 0, 0};
+            // S^T: rows = tokens 16w + 4qq + r of the chunk, columns n; acc3 holds the q3 part
+            v4i acc = {0, 0, 0, 0}, acc3 = {0, 0, 0, 0};
 #pragma unroll
-            for (int jj = 0; jj < 4; jj++)
-                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, b.k[tl][(4 * jj + qq) ^ (tl & 15)]), qi[jj], acc, 0, 0, 0);
-            // the partner column n ^ 8 holds the other part of the same head
+            for (int jj = 0; jj < 4; jj++) {
+                const v4i kop = __builtin_bit_cast(v4i, b.k[tl][(4 * jj + qq) ^ (tl & 15)]);
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop, qi[jj], acc, 0, 0, 0);
+                acc3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop, q3i[jj], acc3, 0, 0, 0);
+            }
+            // the partner column n ^ 8 holds the other part of the same head; every dot is
+            // an integer below 2^22 in magnitude, exact in FP32
             const int local0 = (int)(j * kChunk) + 16 * wave + 4 * qq;   // token offset inside the split
             const uint32_t t0 = begin + (uint32_t)local0;
             float top = -INFINITY;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int mine = acc[r], other = __shfl_xor(mine, 8, 64);
-                const float full = ((float)(lo_col ? other : mine) + (float)(lo_col ? mine : other) * (1.0f / 254.0f)) * qsc;
+                const float hi = (float)(lo_col ? other : mine), lo = (float)(lo_col ? mine : other);
+                const float full = fmaf((float)acc3[r], 1.0f / 64516.0f, fmaf(lo, 1.0f / 254.0f, hi)) * qsc;
                 const float value = t0 + r < end ? full * kscale[local0 + r] : -INFINITY;
                 sc_prev[r] = value;
                 top = fmaxf(top, value);

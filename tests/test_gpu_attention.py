@@ -210,8 +210,6 @@ DECODE_CASES = [(0, 1), (1, 1), (17, 7), (127, 1), (255, 1), (256, 1), (1000, 64
 @pytest.mark.parametrize("path", ["fused", "reference"])
 @pytest.mark.parametrize("history,rows", DECODE_CASES)
 def test_decode_matches_fp64(device, oracle, history, rows, path):
-    if path == "reference" and history > 10000:
-        pytest.skip("three-kernel reader checked on shorter histories")
     q, gate, host = build_case(oracle, history, rows)
     cache = upload_cache(device, *host)
     y = run_decode(device, q, gate, cache, rows, history, path=path)
@@ -275,4 +273,34 @@ def test_decode_long_context_outliers(device, oracle):
     y = run_decode(device, q, gate, cache, 1, length - 1)[:-1]
     ref = oracle.attention(q, kc, vc, ks, vs, gate, 1, length - 1, round_q_half=0)
     assert rel_l2(y, ref) <= REL_L2 and np.abs(y - ref).max() <= MAX_ABS
+    cache.dispose()
+
+
+@pytest.mark.parametrize("history,rows,q_outlier", [(4093, 7, 20.0), (131071, 1, 20.0), (131071, 1, 100.0)])
+def test_decode_query_outliers_match_fp32_reader(device, oracle, history, rows, q_outlier):
+    """Outlier channels in Q as well as K (dims {30,31,62,63} x20 in both, and x100 in Q): one
+    large query dimension sets the split query's scale for its head. The fused decode, whose
+    scores use the three-part INT8 query, stays as close to FP64 as the reference's FP32 scalar
+    reader (kernels.metal:147-156): its error is at most 1.5x the reader's + 1e-6, and both meet
+    the bar."""
+    length = history + rows
+    k, v = outlier_kv(oracle, length, seed=40)
+    kc, vc, ks, vs = oracle.empty_cache(length + 1)
+    oracle.store(k, v, 0, kc, vc, ks, vs)
+    poison_tail(oracle, kc, vc, ks, vs, length)
+    q = oracle.normal(rows * 4096, 41).reshape(rows, 16, 256)
+    q[:, :, [30, 31, 62, 63]] *= np.float32(q_outlier)
+    q = np.ascontiguousarray(q.ravel())
+    gate = oracle.normal(rows * 4096, 42)
+    cache = upload_cache(device, kc, vc, ks, vs)
+    fused = run_decode(device, q, gate, cache, rows, history, path="fused")
+    reader = run_decode(device, q, gate, cache, rows, history, path="reference")
+    assert np.isnan(fused[-1]) and np.isnan(reader[-1])
+    fused, reader = fused[:-1], reader[:-1]
+    ref = oracle.attention(q, kc, vc, ks, vs, gate, rows, history, round_q_half=0)
+    e_fused, e_reader = rel_l2(fused, ref), rel_l2(reader, ref)
+    print(f"decode q-outliers x{q_outlier} ({history},{rows}): fused rel-L2 {e_fused:.3e}, FP32 reader {e_reader:.3e}")
+    assert e_fused <= 1.5 * e_reader + 1e-6, (e_fused, e_reader)
+    assert e_reader <= REL_L2 and np.abs(reader - ref).max() <= MAX_ABS
+    assert np.abs(fused - ref).max() <= MAX_ABS
     cache.dispose()
