@@ -77,6 +77,18 @@ def measured_traffic(kernel: str):
     return int(round((entry["fetch_mb"] + entry["write_mb"]) * 1e6))
 
 
+def measured_counters(kernel: str):
+    """Counter-derived utilisation of ``kernel`` from the committed rocprofv3 PMC summary
+    (profiles/counters.json: MFMA busy, LDS active, bank conflicts), or None."""
+    path = os.path.join(ROOT, "profiles", "counters.json")
+    try:
+        with open(path) as f:
+            entry = json.load(f)["kernels"][kernel]
+    except (OSError, KeyError, ValueError):
+        return None
+    return {k: entry[k] for k in ("mfma_busy", "lds_active", "lds_bank_conflicts_per_access")}
+
+
 def prefill_flops(pos: int, rows: int) -> float:
     # 4 * d * H * sum over rows of visible keys (QK and PV, 2 flop per MAC)
     return 4.0 * 256 * 16 * (rows * pos + rows * (rows + 1) / 2)
@@ -321,6 +333,8 @@ def main():
                      "achieved": round(achieved, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / MFMA_PEAK_TFLOPS, 4),
                      "traffic": measured_traffic("prefill_pp_kernel"),
+                     "mfma_busy": (measured_counters("prefill_pp_kernel") or {}).get("mfma_busy"),
+                     "counters": measured_counters("prefill_pp_kernel"),
                      "flops_per_layer": flops},
     }
     device.reset_wall_timing(kernels_exact=True)
@@ -359,7 +373,8 @@ def main():
             "bound": "hbm", "kernel": "decode_int8_kernel (attention_decode_int8)",
             "achieved": round(bytes_per_dispatch / (dec_kernel_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(bytes_per_dispatch / (dec_kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic("decode_int8_kernel")}
+            "traffic": measured_traffic("decode_int8_kernel"),
+            "counters": measured_counters("decode_int8_kernel")}
         result["roofline_append"] = {
             "bound": "hbm", "kernel": "kv_store_int8 bulk append of 131072 tokens",
             "achieved": round(bulk_bytes / (bulk * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
