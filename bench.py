@@ -15,8 +15,9 @@ Metric: "30K-prefill INT8-KV attn ms/layer (MFMA %); 128K decode
 * roofline: prefill attention kernel against the dense FP16 MFMA peak (2.5 PFLOP/s),
   decode kernel against HBM (8 TB/s); kernel durations from HIP events on the library's
   stream over the timed region.
-* cpu_baseline: the C oracle (FP64, the reference's checker arithmetic) on the host cores,
-  on the last 512-query chunk of config 3, extrapolated by the causal flop ratio.
+* cpu_baseline: the C oracle (FP64, the reference's checker arithmetic) on the host threads,
+  median of 5 runs each of config 1, config 2, one 131072-token decode step, and config 3's
+  last 512-query chunk extrapolated by the causal flop ratio (``value``).
 """
 from __future__ import annotations
 
@@ -148,38 +149,118 @@ class Fp16ControlWorkload:
         d.end()
 
 
-def cpu_baseline_prefill(work: PrefillWorkload, threads: int):
-    """FP64 oracle over the GPU-built INT8 cache: the last chunk of config 3, extrapolated."""
-    sys.path.insert(0, os.path.join(ROOT, "tests"))
-    from oracle_lib import Oracle
-    oracle = Oracle()
-    oracle.threads = threads
-    tokens, chunk = work.tokens, work.chunk
-    pos = tokens - chunk
-    layer = work.layer
-    kc = layer.key.read(np.int8, tokens * 512)
-    vc = layer.value.read(np.int8, engine.int8_value_capacity(tokens) * 512)
-    ks = layer.key_scale.read(np.float32, tokens * 2)
-    vs = layer.value_scale.read(np.float32, tokens * 2)
-    q = work.q.read(np.float32, chunk * 4096, pos * 16384).reshape(chunk, 16, 256).astype(np.float64)
-    # partial RoPE of the queries (Int8KvTests.cs:13-18), vectorised; input preparation is not timed
-    angle = (pos + np.arange(chunk))[:, None] * 10_000_000.0 ** (-2.0 * np.arange(32) / 64)
+def host_threads():
+    """(threads, nproc, affinity) for the CPU baseline: the CPU share the job is granted
+    (OMP_NUM_THREADS where the scheduler sets it, as on the GPU boxes), else every CPU this
+    process may run on."""
+    affinity = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    threads = min(int(env), affinity) if env.isdigit() and int(env) > 0 else affinity
+    return threads, os.cpu_count(), affinity
+
+
+def _spread(times_s):
+    t = sorted(x * 1000.0 for x in times_s)
+    return {"median_ms": round(float(np.median(t)), 3), "min_ms": round(t[0], 3), "max_ms": round(t[-1], 3),
+            "runs": len(t)}
+
+
+def _timed(fn, runs):
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return times
+
+
+def _rotated_queries(q_host, pos):
+    """Partial RoPE of FP32 queries [rows][16][256] at positions pos.. (Int8KvTests.cs:13-18),
+    vectorised in FP64; input preparation, not timed."""
+    q = q_host.astype(np.float64)
+    angle = (pos + np.arange(q.shape[0]))[:, None] * 10_000_000.0 ** (-2.0 * np.arange(32) / 64)
     c, s = np.cos(angle)[:, None, :], np.sin(angle)[:, None, :]
     a, b = q[:, :, :32].copy(), q[:, :, 32:64].copy()
     q[:, :, :32], q[:, :, 32:64] = a * c - b * s, b * c + a * s
-    rot = q.astype(np.float32).ravel()
-    gate = work.gate.read(np.float32, chunk * 4096, pos * 16384)
-    times = []
-    for _ in range(1):
-        t0 = time.perf_counter()
-        oracle.attention(rot, kc, vc, ks, vs, gate, chunk, pos, round_q_half=1)
-        times.append(time.perf_counter() - t0)
-    sample_s = float(np.median(times))
+    return np.ascontiguousarray(q.astype(np.float32).ravel())
+
+
+def cpu_baseline(work: "PrefillWorkload", dec: "DecodeWorkload", runs: int = 5):
+    """The reference's scalar CPU checker restated in C (the oracle: FP64 attention of
+    Int8KvTests.cs:130-158 over the INT8 cache, append of Int8KvTests.cs:116-118), work split over
+    (row, head) for attention and over tokens for append, on the host threads; median of `runs`
+    runs of each workload on the same seeded inputs as the GPU path. ``value`` is config 3 in
+    ms/layer: its last 512-query chunk timed in full and scaled by the causal flop ratio to the
+    whole 30720-token layer (labelled as extrapolated)."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from oracle_lib import Oracle
+    threads, nproc, affinity = host_threads()
+    oracle = Oracle()
+    oracle.threads = threads
+    entries = {}
+
+    # config 1: append 512 tokens of N(0,1) K/V (seed 0/1), one FP32 decode query over all 512
+    k1 = oracle.normal(512 * 512, 0).reshape(512, 2, 256)
+    v1 = oracle.normal(512 * 512, 1).reshape(512, 2, 256)
+    q1, g1 = oracle.normal(4096, 2), np.zeros(4096, np.float32)
+    c1 = oracle.empty_cache(512)
+
+    def config1():
+        oracle.store_mt(k1, v1, 0, *c1)
+        oracle.attention(q1, *c1, g1, 1, 511, round_q_half=0)
+    entries["config1_append512_decode"] = dict(_spread(_timed(config1, runs)), what="append 512 tokens + 1 decode query over 512 keys")
+
+    # config 2: 4096-token causal prompt, 8 chunks of 512 (append + FP16-Q prefill per chunk)
+    k2 = oracle.normal(4096 * 512, 20).reshape(4096, 2, 256)
+    k2[:, :, OUTLIER_CHANNELS] *= 20
+    v2 = oracle.normal(4096 * 512, 21).reshape(4096, 2, 256)
+    q2, g2 = oracle.normal(4096 * 4096, 22), np.zeros(512 * 4096, np.float32)
+    c2 = oracle.empty_cache(4096)
+
+    def config2():
+        for pos in range(0, 4096, 512):
+            oracle.store_mt(k2[pos:pos + 512], v2[pos:pos + 512], pos, *c2)
+            oracle.attention(q2[pos * 4096:(pos + 512) * 4096], *c2, g2, 512, pos, round_q_half=1)
+    entries["config2_prefill4096"] = dict(_spread(_timed(config2, runs)), what="4096-token causal prefill in 8 chunks of 512 (append + attention)")
+
+    # config 4: one decode step at 131072 context over the GPU-built layer (append 1 token +
+    # attention over 131073 keys)
+    if dec is not None:
+        L = dec.context + 1
+        layer = dec.cache.layers[0]
+        cache4 = (layer.key.read(np.int8, L * 512), layer.value.read(np.int8, engine.int8_value_capacity(L) * 512),
+                  layer.key_scale.read(np.float32, L * 2), layer.value_scale.read(np.float32, L * 2))
+        k4 = dec.k_new.read(np.float32, 512).reshape(1, 2, 256)
+        v4 = dec.v_new.read(np.float32, 512).reshape(1, 2, 256)
+        q4 = _rotated_queries(dec.q.read(np.float32, 4096).reshape(1, 16, 256), dec.context)
+        g4 = dec.gate.read(np.float32, 4096)
+
+        def decode_step():
+            oracle.store_mt(k4, v4, dec.context, *cache4)
+            oracle.attention(q4, *cache4, g4, 1, dec.context, round_q_half=0)
+        spread = _spread(_timed(decode_step, runs))
+        spread["kv_read_gbs"] = round(1040 * L / (spread["median_ms"] * 1e-3) / 1e9, 2)
+        entries["config4_decode_step_131072"] = dict(spread, what="append 1 token + decode over 131073 keys (one layer)")
+
+    # config 3: the last 512-query chunk over the GPU-built 30720-token cache, extrapolated
+    tokens, chunk = work.tokens, work.chunk
+    pos = tokens - chunk
+    layer = work.layer
+    cache3 = (layer.key.read(np.int8, tokens * 512), layer.value.read(np.int8, engine.int8_value_capacity(tokens) * 512),
+              layer.key_scale.read(np.float32, tokens * 2), layer.value_scale.read(np.float32, tokens * 2))
+    q3 = _rotated_queries(work.q.read(np.float32, chunk * 4096, pos * 16384).reshape(chunk, 16, 256), pos)
+    g3 = work.gate.read(np.float32, chunk * 4096, pos * 16384)
+    last = _spread(_timed(lambda: oracle.attention(q3, *cache3, g3, chunk, pos, round_q_half=1), runs))
     ratio = work.flops() / prefill_flops(pos, chunk)
-    return {"value": sample_s * ratio * 1000.0, "unit": "ms/layer", "cores": threads, "kind": "port",
-            "sample": f"FP64 oracle (Int8KvTests.cs:130-157 arithmetic) on the last {chunk}-query chunk "
-                      f"(queries {pos}-{tokens - 1} over {tokens} keys, {sample_s:.2f} s), extrapolated x{ratio:.1f} "
-                      f"by the causal flop ratio to the whole 30720-token layer"}
+    last["extrapolated_ms_per_layer"] = round(last["median_ms"] * ratio, 1)
+    entries["config3_last_chunk"] = dict(last, what=f"queries {pos}-{tokens - 1} over {tokens} keys; x{ratio:.2f} causal flop ratio to the layer")
+    return {"value": last["extrapolated_ms_per_layer"], "unit": "ms/layer", "cores": threads, "kind": "port",
+            "nproc": nproc, "affinity_cpus": affinity,
+            "sample": f"C restatement of the reference's FP64 CPU checker (Int8KvTests.cs:116-118,130-158) on {threads} "
+                      f"host threads (nproc {nproc}), median of {runs} runs per workload; value = config 3's last "
+                      f"512-query chunk ({last['median_ms'] / 1000:.2f} s) extrapolated x{ratio:.1f} by the causal flop "
+                      f"ratio to the 30720-token layer",
+            "entries": entries}
 
 
 # --------------------------------------------------------------------------- decode
@@ -255,7 +336,6 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--decode-steps", type=int, default=256,
                     help="decode tokens per timed run (each over every layer); the counter runs "
                          "of the profiles use fewer: traffic per launch does not depend on it")
@@ -382,8 +462,8 @@ def main():
             "traffic": measured_traffic("kv_store_int8 bulk 131072"),
             "bytes": bulk_bytes, "kernel_ms": round(bulk, 4)}
     if not args.no_cpu_baseline:
-        log("cpu baseline: FP64 oracle on the last chunk")
-        result["cpu_baseline"] = cpu_baseline_prefill(work, args.cpu_threads)
+        log("cpu baseline: the FP64 checker on configs 1, 2, a 131072 decode step and config 3's last chunk")
+        result["cpu_baseline"] = cpu_baseline(work, dec)
     print(json.dumps(result), flush=True)
     device.close()
 

@@ -65,6 +65,41 @@ void kvref_store(const float *k, const float *v, int rows, int pos,
     }
 }
 
+typedef struct {
+    const float *k, *v;
+    int rows, pos, first, count;
+    int8_t *kc, *vc;
+    float *ks, *vs;
+} store_job;
+
+static void *store_worker(void *arg) {
+    store_job *j = (store_job *)arg;
+    kvref_store(j->k + (size_t)j->first * 512, j->v + (size_t)j->first * 512, j->count, j->pos + j->first,
+                j->kc, j->vc, j->ks, j->vs);
+    return NULL;
+}
+
+void kvref_store_mt(const float *k, const float *v, int rows, int pos,
+                    int8_t *kc, int8_t *vc, float *ks, float *vs, int threads) {
+    if (threads < 1) threads = 1;
+    if (threads > 256) threads = 256;
+    if (threads > rows) threads = rows > 0 ? rows : 1;
+    store_job jobs[256];
+    pthread_t tid[256];
+    int started[256];
+    int per = (rows + threads - 1) / threads;
+    for (int i = 0; i < threads; i++) {
+        int first = i * per, count = rows - first < per ? rows - first : per;
+        if (count < 0) count = 0;
+        jobs[i] = (store_job){k, v, rows, pos, first, count, kc, vc, ks, vs};
+        started[i] = i > 0 && count > 0 && pthread_create(&tid[i], NULL, store_worker, &jobs[i]) == 0;
+        if (i > 0 && count > 0 && !started[i]) store_worker(&jobs[i]);
+    }
+    if (jobs[0].count > 0) store_worker(&jobs[0]);
+    for (int i = 1; i < threads; i++)
+        if (started[i]) pthread_join(tid[i], NULL);
+}
+
 double kvref_rotate_f64(const float *x, int d, int position) {
     /* Int8KvTests.cs:13-18 */
     if (d >= 64) return x[d];

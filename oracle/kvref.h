@@ -64,6 +64,11 @@ void kvref_quantize(const float *x, int8_t *codes, float *scale);
 void kvref_store(const float *k, const float *v, int rows, int pos,
                  int8_t *kc, int8_t *vc, float *ks, float *vs);
 
+/* kvref_store with the rows split into contiguous blocks over `threads` POSIX threads
+ * (each token's bytes are written by exactly one thread; same bytes as kvref_store). */
+void kvref_store_mt(const float *k, const float *v, int rows, int pos,
+                    int8_t *kc, int8_t *vc, float *ks, float *vs, int threads);
+
 /* FP64 partial RoPE (theta = 1e7, dims 0..63 rotate in pairs j, j+32).
  * Int8KvTests.cs:13-18, KvStorageTests.cs:44-49; GPU form kernels.metal:122-125. */
 double kvref_rotate_f64(const float *x, int d, int position);

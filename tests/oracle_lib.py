@@ -32,6 +32,7 @@ class Oracle:
         lib.kvref_value_bytes.argtypes = [ctypes.c_uint32]
         lib.kvref_quantize.argtypes = [_f32p, _i8p, ctypes.POINTER(ctypes.c_float)]
         lib.kvref_store.argtypes = [_f32p, _f32p, ctypes.c_int, ctypes.c_int, _i8p, _i8p, _f32p, _f32p]
+        lib.kvref_store_mt.argtypes = [_f32p, _f32p, ctypes.c_int, ctypes.c_int, _i8p, _i8p, _f32p, _f32p, ctypes.c_int]
         lib.kvref_rotate_f64.restype = ctypes.c_double
         lib.kvref_rotate_f64.argtypes = [_f32p, ctypes.c_int, ctypes.c_int]
         lib.kvref_half_bits.restype = ctypes.c_uint16
@@ -75,6 +76,12 @@ class Oracle:
         v = np.ascontiguousarray(v, np.float32)
         rows = k.size // 512
         self.lib.kvref_store(k.ravel(), v.ravel(), rows, pos, kc, vc, ks, vs)
+
+    def store_mt(self, k, v, pos, kc, vc, ks, vs):
+        """kvref_store split over ``self.threads`` threads (same bytes)."""
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        self.lib.kvref_store_mt(k.ravel(), v.ravel(), k.size // 512, pos, kc, vc, ks, vs, self.threads)
 
     def empty_cache(self, length: int, fill: int = 0):
         """Host INT8 cache with room for `length` tokens (whole V pages)."""

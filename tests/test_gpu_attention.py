@@ -142,11 +142,11 @@ def test_prefill_small_value_scale(device, oracle):
 
 def test_config2_chunked_prefill(device, oracle):
     """Config 2: 4096-token causal prompt in 8 chunks of 512 with outlier K channels; the cache
-    is appended on the GPU chunk by chunk and every chunk is checked against FP64."""
+    is appended on the GPU chunk by chunk and every chunk is checked against FP64 (gate N(0,1))."""
     total, chunk = 4096, 512
     k, v = outlier_kv(oracle, total, seed=20)
     q_all = oracle.normal(total * 4096, 22)
-    gate_all = np.zeros(total * 4096, np.float32)
+    gate_all = oracle.normal(total * 4096, 23)
     kc, vc, ks, vs = oracle.empty_cache(total)
     cache = upload_cache(device, kc, vc, ks, vs)
     worst_rel, worst_abs = 0.0, 0.0
@@ -163,12 +163,12 @@ def test_config2_chunked_prefill(device, oracle):
         gate = gate_all[pos * 4096:(pos + chunk) * 4096]
         y = run_prefill(device, q, gate, cache, chunk, pos)[:-1]
         oracle.store(k[pos:pos + chunk], v[pos:pos + chunk], pos, kc, vc, ks, vs)
-        if c in (0, 3, 7):
-            ref = oracle.attention(q, kc, vc, ks, vs, gate, chunk, pos, round_q_half=1)
-            worst_rel = max(worst_rel, rel_l2(y, ref))
-            worst_abs = max(worst_abs, float(np.abs(y - ref).max()))
-            # the GPU-appended cache is byte-identical to the oracle's
-            assert cache.kc.read(np.int8, (pos + chunk) * 512).tobytes() == kc[:(pos + chunk) * 512].tobytes()
+        ref = oracle.attention(q, kc, vc, ks, vs, gate, chunk, pos, round_q_half=1)
+        worst_rel = max(worst_rel, rel_l2(y, ref))
+        worst_abs = max(worst_abs, float(np.abs(y - ref).max()))
+        # the GPU-appended cache is byte-identical to the oracle's
+        assert cache.kc.read(np.int8, (pos + chunk) * 512).tobytes() == kc[:(pos + chunk) * 512].tobytes()
+        assert cache.vs.read(np.float32, (pos + chunk) * 2).tobytes() == vs[:(pos + chunk) * 2].tobytes()
     assert worst_rel <= REL_L2 and worst_abs <= MAX_ABS, (worst_rel, worst_abs)
     cache.dispose()
 

@@ -35,7 +35,8 @@ def test_batch_rope_fp16_storage(device, oracle):
         b.dispose()
 
 
-@pytest.mark.parametrize("history,rows", [(0, 1), (17, 7), (127, 33), (257, 64), (4093, 7), (8192, 128), (3584, 512)])
+@pytest.mark.parametrize("history,rows", [(0, 1), (17, 7), (127, 33), (257, 64), (4093, 7), (8192, 128), (3584, 512),
+                                          (30208, 512)])
 def test_online_fp16_matches_fp64(device, oracle, history, rows):
     length = history + rows
     k = oracle.fill_hash(length * 512, 31, 3)       # OnlineAttentionTests.cs:26-27 fills

@@ -367,3 +367,20 @@ def test_probability_operand_rounding_against_the_bar(oracle, history, rows):
     assert rel_l2(bf16, ref) > 1.5e-3
     assert np.all(np.abs(bf16 - ref) <= bound / 256 + 1e-4)
     assert rel_l2(fp16, ref) < 2.5e-4 and np.abs(fp16 - ref).max() < 2e-4
+
+
+def test_threaded_store_writes_the_same_bytes(oracle):
+    """kvref_store_mt (the CPU baseline's append, split over tokens) equals kvref_store."""
+    rng = np.random.default_rng(13)
+    rows, pos = 300, 77
+    k = rng.standard_normal((rows, 2, 256)).astype(np.float32)
+    v = rng.standard_normal((rows, 2, 256)).astype(np.float32)
+    a = oracle.empty_cache(pos + rows, fill=0x55)
+    b = oracle.empty_cache(pos + rows, fill=0x55)
+    oracle.store(k, v, pos, *a)
+    saved = oracle.threads
+    for threads in (1, 7, 16):
+        oracle.threads = threads
+        oracle.store_mt(k, v, pos, *b)
+        assert all(x.tobytes() == y.tobytes() for x, y in zip(a, b))
+    oracle.threads = saved
