@@ -51,6 +51,8 @@ SIGNATURES = {
     "boot_clear": (_I, [_VP, _VP]),
     "boot_dispatch": (_I, [_VP, _CP, ctypes.POINTER(_VP), ctypes.POINTER(_U64), _I, _VP, _I,
                            _U32, _U32, _U32, _U32, _U32, _U32, _VP, _U64]),
+    "boot_dispatch_noalloc": (_I, [_VP, _CP, ctypes.POINTER(_VP), ctypes.POINTER(_U64), _I, _VP, _I,
+                                   _U32, _U32, _U32, _U32, _U32, _U32, _VP, _U64]),
     "boot_end": (_I, [_VP]),
     "boot_profile": (None, [_VP, _I]),
     "boot_wall_reset": (_I, [_VP, _I]),
@@ -204,13 +206,15 @@ class Device:
     def copy(self, dst: GpuBuffer, dst_offset: int, src: GpuBuffer, src_offset: int, nbytes: int) -> None:
         self._check(self.lib.boot_copy(self.handle, dst.handle, dst_offset, src.handle, src_offset, nbytes))
 
-    def dispatch(self, kernel: str, args: KernelArgs, threads: int, group: int, *bindings) -> None:
+    def dispatch(self, kernel: str, args: KernelArgs, threads: int, group: int, *bindings,
+                 noalloc: bool = False) -> None:
         """Metal.cs:96-97."""
-        self.dispatch2d(kernel, args, threads, 1, group, *bindings)
+        self.dispatch2d(kernel, args, threads, 1, group, *bindings, noalloc=noalloc)
 
     def dispatch2d(self, kernel: str, args: KernelArgs, threads_x: int, threads_y: int, group: int,
-                   *bindings) -> None:
-        """Metal.cs:98-104."""
+                   *bindings, noalloc: bool = False) -> None:
+        """Metal.cs:98-104. ``noalloc`` routes through boot_dispatch_noalloc (split-K scratch
+        from the library's static device array; no allocation, no timing sample)."""
         count = len(bindings)
         handles = (ctypes.c_void_p * max(count, 1))()
         offsets = (ctypes.c_uint64 * max(count, 1))()
@@ -219,9 +223,9 @@ class Device:
                 b = Binding(b, 0)
             handles[i] = b.buffer.handle
             offsets[i] = b.offset
-        self._check(self.lib.boot_dispatch(self.handle, kernel.encode(), handles, offsets, count,
-                                           ctypes.byref(args), ctypes.sizeof(KernelArgs),
-                                           threads_x, threads_y, 1, group, 1, 1, None, 0))
+        entry = self.lib.boot_dispatch_noalloc if noalloc else self.lib.boot_dispatch
+        self._check(entry(self.handle, kernel.encode(), handles, offsets, count, ctypes.byref(args),
+                          ctypes.sizeof(KernelArgs), threads_x, threads_y, 1, group, 1, 1, None, 0))
 
     def close(self) -> None:
         """Metal.cs:114. boot_destroy frees the context and every buffer it still owns, so the

@@ -13,6 +13,7 @@
 
 #include <chrono>
 #include <map>
+#include <mutex>
 #include <string>
 #include <unordered_map>
 #include <unordered_set>
@@ -21,6 +22,42 @@
 #include "common.h"
 
 namespace boot {
+
+// Split-K scratch of boot_dispatch_noalloc (the attention kernels' per-split partials): 48 MiB,
+// enough for every prefill chunk on 256 CUs (one partial of at most 134,144 bytes per CU) and
+// for single-token decode up to the 262144 window (about 2 MiB). Each device holds its own copy
+// until the process ends; the host reaches it only through the address kept per device below.
+constexpr uint64_t kStaticScratchBytes = 48ull << 20;
+
+}  // namespace boot
+
+static __device__ __align__(256) unsigned char scratch[boot::kStaticScratchBytes];
+
+namespace boot {
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::once_flag scratch_once[kMaxDevices];
+void *scratch_address[kMaxDevices];
+hipError_t scratch_status[kMaxDevices];
+
+// Device address of `scratch` on the current device, looked up once per device (the array's
+// name is a host-side stand-in, never a device address). Null with the HIP error if the lookup
+// failed.
+void *static_scratch(int device, hipError_t *status) {
+    if (device < 0 || device >= kMaxDevices) {
+        *status = hipErrorInvalidDevice;
+        return nullptr;
+    }
+    std::call_once(scratch_once[device], [device] {
+        void *ptr = nullptr;
+        scratch_status[device] = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        scratch_address[device] = scratch_status[device] == hipSuccess ? ptr : nullptr;
+    });
+    *status = scratch_status[device];
+    return scratch_address[device];
+}
+}  // namespace
 
 struct Buffer {
     Context *ctx;
@@ -44,6 +81,12 @@ struct Context {
     uint64_t allocated = 0;
     void *workspace = nullptr;
     uint64_t workspace_bytes = 0;
+    // boot_dispatch_noalloc: the device's static scratch replaces the workspace and no
+    // timing event is recorded while `noalloc` is set
+    bool noalloc = false;
+    void *scratch = nullptr;
+    hipError_t scratch_status = hipSuccess;
+    uint64_t scratch_request = 0;   // bytes the last refused request asked for
     // serialized per-dispatch profiling (bridge.mm:61,198-204)
     bool profile = false;
     std::map<std::string, std::pair<double, uint64_t>> timings;
@@ -141,6 +184,13 @@ hipStream_t context_stream(Context &c) { return c.stream; }
 int context_cus(Context &c) { return c.cus; }
 
 void *context_workspace(Context &c, uint64_t bytes) {
+    if (c.noalloc) {
+        if (!c.scratch || bytes > kStaticScratchBytes) {
+            c.scratch_request = bytes;
+            return nullptr;
+        }
+        return c.scratch;
+    }
     if (bytes <= c.workspace_bytes) return c.workspace;
     // Grow: the old scratch may still be read by enqueued work.
     if (hipStreamSynchronize(c.stream) != hipSuccess) return nullptr;
@@ -162,7 +212,7 @@ void *context_workspace(Context &c, uint64_t bytes) {
 
 void context_kernel_events(Context &c, const char *kernel, hipEvent_t *start, hipEvent_t *stop) {
     *start = *stop = nullptr;
-    if (!c.wall_enabled || c.sample_mode != 3 || !c.active) return;
+    if (c.noalloc || !c.wall_enabled || c.sample_mode != 3 || !c.active) return;
     hipEvent_t a = next_event(&c), b = next_event(&c);
     if (!a || !b) return;
     *start = a;
@@ -173,7 +223,7 @@ void context_kernel_events(Context &c, const char *kernel, hipEvent_t *start, hi
 // Ends the current sample of a multi-kernel dispatch and starts one named
 // `name` (used to time a split-K combine apart from its main kernel).
 void context_split(Context &c, const char *name) {
-    if (!c.sampling) return;
+    if (c.noalloc || !c.sampling) return;
     hipEvent_t e = record(&c);
     c.samples.push_back({c.current_name, c.current_start, e, c.current_kind});
     c.current_name = name;
@@ -203,6 +253,9 @@ void *boot_create(const char *source) {
     if (hipSetDevice(0) != hipSuccess) return nullptr;
     Context *c = new Context();
     c->cus = prop.multiProcessorCount;
+    // the static scratch of boot_dispatch_noalloc, once per device with it current; a failed
+    // lookup fails only that entry point (with this error)
+    c->scratch = static_scratch(0, &c->scratch_status);
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
         delete c;
         return nullptr;
@@ -371,18 +424,28 @@ int boot_clear(void *handle, void *buffer) {
     return hip_ok(c, fill_zero(b->ptr, b->bytes, c->stream), "boot_clear");
 }
 
-int boot_dispatch(void *handle, const char *name, void **buffers, const uint64_t *offsets, int count,
-                  const void *parameters, int parameter_bytes, uint32_t x, uint32_t y, uint32_t z,
-                  uint32_t tx, uint32_t ty, uint32_t tz, void *indirect, uint64_t indirect_offset) {
-    Context *c = static_cast<Context *>(handle);
-    (void)indirect_offset;
+}  // extern "C"
+
+namespace {
+
+// boot_dispatch and boot_dispatch_noalloc. With `noalloc` the kernel name is matched without
+// building strings, no timing event is recorded and split-K launchers draw their partials from
+// the device's static scratch, so the call allocates no device or host memory unless it fails.
+int dispatch(Context *c, const char *name, void **buffers, const uint64_t *offsets, int count,
+             const void *parameters, int parameter_bytes, uint32_t x, uint32_t y, uint32_t z,
+             uint32_t tx, uint32_t ty, uint32_t tz, void *indirect, bool noalloc) {
     if (!c->active) return fail(c, "boot_dispatch requires an active command");
-    auto found = registry().find(name ? name : "");
-    if (found == registry().end()) return fail(c, std::string("Unknown kernel: ") + (name ? name : "(null)"));
+    const Entry *entry = nullptr;
+    for (auto &item : registry())
+        if (name && strcmp(item.first.c_str(), name) == 0) entry = &item.second;
+    if (!entry) return fail(c, std::string("Unknown kernel: ") + (name ? name : "(null)"));
     if (indirect) return fail(c, std::string(name) + ": indirect dispatch is not supported by INT8 kernels");
     if (count < 0 || count > 31) return fail(c, std::string(name) + ": invalid binding count");
     if (!parameters || parameter_bytes < (int)sizeof(boot_kernel_args))
         return fail(c, std::string(name) + ": argument block must be 64 bytes");
+    if (noalloc && !c->scratch)
+        return fail(c, std::string("boot_dispatch_noalloc: static scratch unavailable: ") +
+                           hipGetErrorString(c->scratch_status));
     View views[32];
     for (int i = 0; i < count; i++) {
         Buffer *b = as_buffer(c, buffers[i]);
@@ -394,26 +457,37 @@ int boot_dispatch(void *handle, const char *name, void **buffers, const uint64_t
     boot_kernel_args p;
     memcpy(&p, parameters, sizeof p);
     const uint32_t grid[6] = {x, y, z, tx, ty, tz};
-    const bool sample = c->wall_enabled && (c->sample_mode == 2 || (c->sample_mode == 1 && found->second.kind >= 0));
+    const bool sample = !noalloc && c->wall_enabled &&
+                        (c->sample_mode == 2 || (c->sample_mode == 1 && entry->kind >= 0));
+    const bool serial = !noalloc && c->profile;
     hipEvent_t serial_start = nullptr;
-    if (c->profile) serial_start = record(c);
+    if (serial) serial_start = record(c);
     if (sample) {
         c->sampling = true;
         c->current_name = name;
-        c->current_kind = found->second.kind;
+        c->current_kind = entry->kind;
         c->current_start = record(c);
     }
-    const char *message = found->second.launch(*c, views, count, p, grid);
+    c->noalloc = noalloc;
+    const char *message = entry->launch(*c, views, count, p, grid);
+    c->noalloc = false;
     if (sample) {
         hipEvent_t e = record(c);
         c->samples.push_back({c->current_name, c->current_start, e, c->current_kind});
         c->sampling = false;
     }
+    if (message && noalloc && c->scratch_request > kStaticScratchBytes) {
+        const uint64_t asked = c->scratch_request;
+        c->scratch_request = 0;
+        return fail(c, std::string(name) + ": split partials need " + std::to_string(asked) +
+                           " bytes, more than the " + std::to_string(kStaticScratchBytes) +
+                           "-byte static scratch of boot_dispatch_noalloc");
+    }
     if (message) return fail(c, std::string(name) + ": " + message);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(c, std::string(name) + ": launch failed: " + hipGetErrorString(e));
     if (c->wall_enabled) c->wall[5]++;
-    if (c->profile) {
+    if (serial) {
         hipEvent_t stop = record(c);
         if (!hip_ok(c, hipEventSynchronize(stop), name)) return 0;
         float ms = 0;
@@ -424,6 +498,26 @@ int boot_dispatch(void *handle, const char *name, void **buffers, const uint64_t
         c->events_used = 0;
     }
     return 1;
+}
+
+}  // namespace
+
+extern "C" {
+
+int boot_dispatch(void *handle, const char *name, void **buffers, const uint64_t *offsets, int count,
+                  const void *parameters, int parameter_bytes, uint32_t x, uint32_t y, uint32_t z,
+                  uint32_t tx, uint32_t ty, uint32_t tz, void *indirect, uint64_t indirect_offset) {
+    (void)indirect_offset;
+    return dispatch(static_cast<Context *>(handle), name, buffers, offsets, count, parameters, parameter_bytes, x, y,
+                    z, tx, ty, tz, indirect, false);
+}
+
+int boot_dispatch_noalloc(void *handle, const char *name, void **buffers, const uint64_t *offsets, int count,
+                          const void *parameters, int parameter_bytes, uint32_t x, uint32_t y, uint32_t z,
+                          uint32_t tx, uint32_t ty, uint32_t tz, void *indirect, uint64_t indirect_offset) {
+    (void)indirect_offset;
+    return dispatch(static_cast<Context *>(handle), name, buffers, offsets, count, parameters, parameter_bytes, x, y,
+                    z, tx, ty, tz, indirect, true);
 }
 
 int boot_end(void *handle) {

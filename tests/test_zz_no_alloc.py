@@ -1,0 +1,87 @@
+"""boot_dispatch_noalloc (the entry point that allocates nothing) against boot_dispatch on the
+same inputs: split-K decode and prefill, two calls in a row with the second smaller, results
+bitwise equal and within the FP64 bar; sizes beyond the static scratch are refused."""
+import numpy as np
+import pytest
+
+from bootstrap_hip import HipError, KernelArgs
+from kvcase import outlier_kv, poison_tail, reference_kv, rel_l2, upload, upload_cache
+
+pytestmark = pytest.mark.gpu
+
+
+def host_cache(oracle, length, kv):
+    kc, vc, ks, vs = oracle.empty_cache(length + 1)
+    oracle.store_mt(*kv, 0, kc, vc, ks, vs)
+    poison_tail(oracle, kc, vc, ks, vs, length)
+    return kc, vc, ks, vs
+
+
+def decode(device, q, gate, cache, rows, history, noalloc):
+    qb, gb = upload(device, q), upload(device, gate)
+    out = device.allocate(q.nbytes + 4)
+    out.write(np.full(rows * 4096 + 1, np.nan, np.float32))
+    device.begin()
+    device.dispatch("attention_decode_int8", KernelArgs(M=rows, K=history + rows, Position=history), rows * 4096, 256,
+                    qb, cache.kc, cache.vc, gb, out, cache.ks, cache.vs, noalloc=noalloc)
+    device.end()
+    y = out.read(np.float32, rows * 4096 + 1)
+    for b in (qb, gb, out):
+        b.dispose()
+    assert np.isnan(y[-1])
+    return y[:-1]
+
+
+def prefill(device, q, gate, cache, rows, history, noalloc):
+    qb, gb = upload(device, q), upload(device, gate)
+    packed, out = device.allocate(rows * 8192), device.allocate(q.nbytes + 4)
+    out.write(np.full(rows * 4096 + 1, np.nan, np.float32))
+    p = KernelArgs(M=rows, K=history + rows, Position=history, A=8)
+    device.begin()
+    device.dispatch("attention_query_grouped_half", p, rows * 1024, 128, qb, packed, noalloc=noalloc)
+    device.dispatch2d("attention_online_int8_q32_k256_r2", p, (rows * 8 + 31) // 32 * 256, 2, 256, packed, cache.kc,
+                      cache.vc, gb, out, cache.ks, cache.vs, noalloc=noalloc)
+    device.end()
+    y = out.read(np.float32, rows * 4096 + 1)
+    for b in (qb, gb, packed, out):
+        b.dispose()
+    assert np.isnan(y[-1])
+    return y[:-1]
+
+
+@pytest.mark.parametrize("kind,cases", [
+    ("decode", [(131071, 1), (4093, 7)]),        # 114 splits per group, then 6
+    ("prefill", [(30208, 512), (257, 33)]),      # 34.3 MB of partials, then 8 splits of one tile
+])
+def test_noalloc_matches_dispatch(device, oracle, kind, cases):
+    run = decode if kind == "decode" else prefill
+    for history, rows in cases:
+        length = history + rows
+        kv = outlier_kv(oracle, length, seed=70) if length > 100000 else reference_kv(length)
+        host = host_cache(oracle, length, kv)
+        cache = upload_cache(device, *host)
+        q = oracle.fill_hash(rows * 4096, 17, 3)
+        gate = oracle.fill_hash(rows * 4096, 11, 1)
+        expected = run(device, q, gate, cache, rows, history, noalloc=False)
+        got = run(device, q, gate, cache, rows, history, noalloc=True)
+        assert np.array_equal(got.view(np.uint32), expected.view(np.uint32)), (kind, history, rows)
+        ref = oracle.attention(q, *host, gate, rows, history, round_q_half=1 if kind == "prefill" else 0)
+        assert rel_l2(got, ref) <= 1e-3 and np.abs(got - ref).max() <= 2e-3
+        cache.dispose()
+
+
+def test_noalloc_refuses_beyond_the_static_scratch(device, oracle):
+    """64 decode rows at the full window need 2 x 64 x 128 split partials of 8256 bytes
+    (135 MB): refused on the host with the size, before any launch; the context stays usable."""
+    rows, history = 64, 262144 - 64
+    k = device.allocate(262144 * 512)
+    v = device.allocate(262144 * 512)
+    scales = [device.allocate(262144 * 8) for _ in range(2)]
+    q, gate, out = device.allocate(rows * 16384), device.allocate(rows * 16384), device.allocate(rows * 16384)
+    device.begin()
+    with pytest.raises(HipError, match="static scratch"):
+        device.dispatch("attention_decode_int8", KernelArgs(M=rows, K=history + rows, Position=history), rows * 4096,
+                        256, q, k, v, gate, out, *scales, noalloc=True)
+    device.end()
+    for b in (k, v, q, gate, out, *scales):
+        b.dispose()
