@@ -4,11 +4,12 @@
 Metric (BASELINE.json): "30K-prefill INT8-KV attn ms/layer (MFMA %); 128K decode KV-read GB/s".
 
 * step (``value``, ms per layer): config 3 — a 30720-token causal prompt of one
-  full-attention layer in 60 chunks of 512 tokens. Per chunk, exactly the engine's
-  INT8 sequence (Prefill.cs:255-261): batch_rope_int8 (rotate Q, rotate K, INT8 append)
-  -> attention_query_grouped_half -> attention_online_int8 (+ split combine).
-  Inputs (FP32 Q/K/V, gate) are resident in HBM before timing; synthetic N(0,1) with
-  K channels {30,31,62,63} x 20; 16 Q / 2 KV heads, d = 256.
+  full-attention layer in 60 chunks of 512 tokens. Per chunk, the engine's INT8 sequence
+  with fused preparation, the one the reference measured at 30K (Prefill.cs:249-251,261):
+  attention_prepare_fused_int8 (norm, RoPE, grouped FP16 Q, gate, INT8 append) ->
+  attention_online_int8 on the prepared query (+ split combine). Inputs (FP32 qkv, K, V)
+  are resident in HBM before timing; synthetic N(0,1) with K channels {30,31,62,63} x 20;
+  16 Q / 2 KV heads, d = 256.
 * decode (extra keys): config 4 — cache grown from 4096 tokens by doubling with device
   copies while being filled to 131072 tokens, pre-grown to 262144, then 256 sequential
   single-token steps (batch_rope_int8 append + attention_decode_int8) over L = 131073..131328.
@@ -98,15 +99,24 @@ def prefill_flops(pos: int, rows: int) -> float:
 # --------------------------------------------------------------------------- prefill
 
 class PrefillWorkload:
+    """Config 3 per chunk as the reference's measured 30K INT8 run issues it (fused preparation,
+    Prefill.cs:249-251,261; 160 attention calls among 340 attention-and-preparation dispatches,
+    docs/INT8_30K_NEXT_PROFILE_20261104.md:36-45): attention_prepare_fused_int8 (Q/K RMS norm,
+    RoPE, grouped FP16 Q, gate split, INT8 append) -> attention_online_int8_q32_k256_r2 on the
+    prepared query (+ split combine). Synthetic qkv [tokens][16][q|gate][256], K with outlier
+    channels, V, all ~N(0,1); norm weights 0 (RMS normalisation with w + 1 = 1)."""
+
     def __init__(self, device, tokens=30720, chunk=512, seed=0):
         self.device, self.tokens, self.chunk = device, tokens, chunk
         rng = np.random.default_rng(seed)
-        log(f"prefill: generating {tokens} tokens of synthetic Q/K/V/gate")
-        self.q = upload(device, synthetic(rng, (tokens, 16, 256)))
+        log(f"prefill: generating {tokens} tokens of synthetic qkv/K/V")
+        self.qkv = upload(device, synthetic(rng, (tokens, 8192)))
         self.k = upload(device, synthetic(rng, (tokens, 2, 256), outliers=True))
         self.v = upload(device, synthetic(rng, (tokens, 2, 256)))
-        self.gate = upload(device, synthetic(rng, (tokens, 16, 256)))
-        self.rotated = device.allocate(tokens * 4096 * 4)
+        self.q_norm = upload(device, np.zeros(256, np.uint16))
+        self.k_norm = upload(device, np.zeros(256, np.uint16))
+        self.gate = device.allocate(chunk * 16384)          # the chunk's gate, split out by the preparation
+        self.out = device.allocate(chunk * 16384)           # the chunk's attention output
         self.cache = engine.Int8KvCache(device, context_window=engine.NATIVE_WINDOW, layers=1)
         self.cache.ensure_capacity(tokens)
         self.layer = self.cache.layers[0]
@@ -114,15 +124,14 @@ class PrefillWorkload:
         self.workspace.prepare(chunk)
 
     def step(self):
-        d, layer = self.device, self.layer
+        d, layer, ws = self.device, self.layer, self.workspace
         d.begin()
         for pos in range(0, self.tokens, self.chunk):
             rows = min(self.chunk, self.tokens - pos)
-            q = self.q.at(pos * 16384)
-            rot = self.rotated.at(pos * 16384)
-            engine.append_rows(d, layer, q, self.k.at(pos * 2048), self.v.at(pos * 2048), rot, rows, pos)
-            self.workspace.encode_int8(rot, layer.key, layer.value, layer.key_scale, layer.value_scale,
-                                       self.gate.at(pos * 16384), rot, rows, pos)
+            engine.prepare_fused(d, layer, self.qkv.at(pos * 32768), self.k.at(pos * 2048), self.v.at(pos * 2048),
+                                 self.q_norm, self.k_norm, ws.packed_query, self.gate, rows, pos)
+            ws.encode_int8(None, layer.key, layer.value, layer.key_scale, layer.value_scale, self.gate, self.out,
+                           rows, pos, prepared_query=True)
         d.end()
 
     def flops(self):
@@ -130,8 +139,9 @@ class PrefillWorkload:
 
 
 class Fp16ControlWorkload:
-    """The same prompt with FP16 KV storage (config 3's side-by-side comparator): per chunk
-    batch_rope (flags 256) -> attention_query_grouped_half -> attention_online_q32_k256_s8_g8_r2."""
+    """The same prompt with FP16 KV storage (config 3's side-by-side comparator), in the same
+    shape: attention_prepare_fused (FP16 K/V) -> attention_online_q32_k256_s8_g8_r2 on the
+    prepared query (+ split combine)."""
 
     def __init__(self, work: PrefillWorkload):
         self.work = work
@@ -142,10 +152,9 @@ class Fp16ControlWorkload:
         d.begin()
         for pos in range(0, w.tokens, w.chunk):
             rows = min(w.chunk, w.tokens - pos)
-            rot = w.rotated.at(pos * 16384)
-            engine.append_rows_fp16(d, self.layer, w.q.at(pos * 16384), w.k.at(pos * 2048), w.v.at(pos * 2048), rot,
-                                    rows, pos)
-            engine.encode_online_fp16(w.workspace, rot, self.layer, w.gate.at(pos * 16384), rot, rows, pos)
+            engine.prepare_fused_fp16(d, self.layer, w.qkv.at(pos * 32768), w.k.at(pos * 2048), w.v.at(pos * 2048),
+                                      w.q_norm, w.k_norm, w.workspace.packed_query, w.gate, rows, pos)
+            engine.encode_online_fp16(w.workspace, None, self.layer, w.gate, w.out, rows, pos, prepared_query=True)
         d.end()
 
 
@@ -248,8 +257,10 @@ def cpu_baseline(work: "PrefillWorkload", dec: "DecodeWorkload", runs: int = 5):
     layer = work.layer
     cache3 = (layer.key.read(np.int8, tokens * 512), layer.value.read(np.int8, engine.int8_value_capacity(tokens) * 512),
               layer.key_scale.read(np.float32, tokens * 2), layer.value_scale.read(np.float32, tokens * 2))
-    q3 = _rotated_queries(work.q.read(np.float32, chunk * 4096, pos * 16384).reshape(chunk, 16, 256), pos)
-    g3 = work.gate.read(np.float32, chunk * 4096, pos * 16384)
+    # the last chunk's prepared query (grouped FP16 [2][rows][8][256], as the GPU attended it) and gate
+    packed = work.workspace.packed_query.read(np.float16, chunk * 4096).reshape(2, chunk, 8, 256)
+    q3 = np.ascontiguousarray(packed.transpose(1, 0, 2, 3).astype(np.float32).ravel())
+    g3 = work.gate.read(np.float32, chunk * 4096)
     last = _spread(_timed(lambda: oracle.attention(q3, *cache3, g3, chunk, pos, round_q_half=1), runs))
     ratio = work.flops() / prefill_flops(pos, chunk)
     last["extrapolated_ms_per_layer"] = round(last["median_ms"] * ratio, 1)
@@ -389,8 +400,7 @@ def main():
     device.reset_wall_timing(kernels_exact=True)
     for _ in range(args.steps):
         work.step()
-    ks = kernel_stats(device, ["prefill_pp_kernel", "prefill_combine_half_kernel", "batch_rope_int8_kernel",
-                               "query_grouped_half_kernel"])
+    ks = kernel_stats(device, ["prefill_pp_kernel", "prefill_combine_half_kernel", "prepare_fused_int8_kernel"])
     attn_ms = ks["prefill_pp_kernel"][0] / args.steps
     combine_ms = ks.get("prefill_combine_half_kernel", (0.0, 0))[0] / args.steps
     launches = ks["prefill_pp_kernel"][1] // args.steps
@@ -401,12 +411,11 @@ def main():
         "warmup": args.warmup, "ms_per_step": round(wall_ms, 4), "higher_is_better": False, "scaling": "weak",
         "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
         "config": {"workload": "config 3: 30720-token causal prefill of one full-attention layer, 60 chunks of 512, "
-                               "INT8 KV (append + online attention), 16 Q / 2 KV heads, d=256",
+                               "INT8 KV (fused preparation with append + online attention), 16 Q / 2 KV heads, d=256",
                    "kv": "int8 + fp32 per-token/head scales", "tokens": 30720, "chunk": 512,
                    "parallelism": "single GPU"},
         "prefill": {"attention_kernel_ms_per_layer": round(attn_ms, 4), "combine_ms_per_layer": round(combine_ms, 4),
-                    "append_ms_per_layer": round(ks["batch_rope_int8_kernel"][0] / args.steps, 4),
-                    "query_pack_ms_per_layer": round(ks["query_grouped_half_kernel"][0] / args.steps, 4),
+                    "prepare_ms_per_layer": round(ks["prepare_fused_int8_kernel"][0] / args.steps, 4),
                     "attention_launches_per_layer": launches,
                     "mfma_fraction_end_to_end": round(flops / (wall_ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4)},
         "roofline": {"bound": "mfma", "kernel": "prefill_pp_kernel (attention_online_int8_q32_k256_r2)",
@@ -420,12 +429,12 @@ def main():
     device.reset_wall_timing(kernels_exact=True)
     for _ in range(args.steps):
         control.step()
-    kc = kernel_stats(device, ["prefill_fp16_kernel", "prefill_combine_kernel<128>", "batch_rope_half_kernel"])
+    kc = kernel_stats(device, ["prefill_fp16_kernel", "prefill_combine_kernel<128>", "prepare_fused_half_kernel"])
     result["fp16_kv_control"] = {
         "ms_per_layer": round(fp16_ms, 4),
         "attention_kernel_ms_per_layer": round(kc["prefill_fp16_kernel"][0] / args.steps, 4),
         "combine_ms_per_layer": round(kc.get("prefill_combine_kernel<128>", (0.0, 0))[0] / args.steps, 4),
-        "append_ms_per_layer": round(kc["batch_rope_half_kernel"][0] / args.steps, 4),
+        "prepare_ms_per_layer": round(kc["prepare_fused_half_kernel"][0] / args.steps, 4),
         "int8_over_fp16_time": round(wall_ms / fp16_ms, 4),
         "kv_bytes_30k": {"int8_with_scales": 30720 * 1040, "fp16": 30720 * 2048}}
     if dec is not None:

@@ -353,6 +353,15 @@ def prepare_fused(device: Device, layer: Int8KvLayer, qkv, k, v, q_norm, k_norm,
                     gate, layer.key, layer.value, layer.key_scale, layer.value_scale)
 
 
+def prepare_fused_fp16(device: Device, layer: "Fp16KvLayer", qkv, k, v, q_norm, k_norm, packed, gate, rows: int,
+                       position: int, theta: float = ROPE_THETA, epsilon: float = 1e-6) -> None:
+    """Fused FP16-KV preparation of Prefill.cs:252 (attention_prepare_fused): Q/K RMS norm with
+    (w + 1), RoPE, grouped FP16 Q + gate split, FP16 K/V append. Inside a command."""
+    p = KernelArgs(M=rows, Position=position, K=position + rows, Theta=theta, Epsilon=epsilon, A=GROUP)
+    device.dispatch("attention_prepare_fused", p, rows * 18 * 256, 256, qkv, k, v, q_norm, k_norm, packed, gate,
+                    layer.key, layer.value)
+
+
 def store_rows(device: Device, layer: Int8KvLayer, k, v, rows: int, position: int) -> None:
     """Append already-rotated FP32 K/V rows (store_kv_int8 alone). Inside a command."""
     device.dispatch("kv_store_int8", KernelArgs(M=rows, Position=position), rows * 512, 256,

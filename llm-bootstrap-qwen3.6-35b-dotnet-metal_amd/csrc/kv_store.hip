@@ -224,18 +224,17 @@ __global__ __launch_bounds__(256) void batch_rope_int8_kernel(
     __shared__ __attribute__((aligned(16))) uint8_t vt[256 * vt_stride<kTile>()];
     const float ifreq = lane_inv_freq(theta);
     if (blockIdx.x < qblocks) {
-        // one wave per row: the angles are computed once and reused by its 16 heads
-        const int lane = threadIdx.x & 63;
-        const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
-        if (row >= rows) return;                                     // wave-uniform
+        // one work-group per row, wave w rotating heads 4w..4w+3 (loads issued together)
+        const int lane = threadIdx.x & 63, h0 = 4 * (threadIdx.x >> 6);
+        const uint32_t row = blockIdx.x;
         const Rope4 r = rope_angles(pos + row, lane, ifreq);
-        const float *src = q + (size_t)row * 4096 + 4 * lane;
-        float *dst = qr + (size_t)row * 4096 + 4 * lane;
-        float4 x[16];
+        const float *src = q + (size_t)row * 4096 + h0 * 256 + 4 * lane;
+        float *dst = qr + (size_t)row * 4096 + h0 * 256 + 4 * lane;
+        float4 x[4];
 #pragma unroll
-        for (int h = 0; h < 16; h++) x[h] = *reinterpret_cast<const float4 *>(src + h * 256);
+        for (int h = 0; h < 4; h++) x[h] = *reinterpret_cast<const float4 *>(src + h * 256);
 #pragma unroll
-        for (int h = 0; h < 16; h++) *reinterpret_cast<float4 *>(dst + h * 256) = rope4(x[h], lane, r);
+        for (int h = 0; h < 4; h++) *reinterpret_cast<float4 *>(dst + h * 256) = rope4(x[h], lane, r);
         return;
     }
     const uint32_t b = blockIdx.x - qblocks;
@@ -247,6 +246,34 @@ __global__ __launch_bounds__(256) void batch_rope_int8_kernel(
 // split) and the 2 KV heads (RMS norm with k_norm, RoPE, INT8 append). One wave
 // per row rotates its 16 query heads with one set of angles; K/V use the
 // page-tiled store. q holds [rows][16][q 256 | gate 256] (kernels.metal:1904).
+// Query half of the fused preparations (kernels.metal:1896-1900 / 1907-1911): work-group `row`,
+// wave w takes heads 4w..4w+3 with all their loads issued together; each head is RMS-normalized
+// with (w + 1), rotated, written as grouped FP16 [(h/8*rows+row)*8+h%8][256], and its gate half
+// copied out. The per-head arithmetic is rmsnorm's and batch_rope_int8's, so the fused and the
+// unfused chains give the same bits.
+__device__ __attribute__((always_inline)) inline void prepare_query_heads(
+    const float *__restrict__ qkv, const uint16_t *__restrict__ qw, _Float16 *__restrict__ packed,
+    float *__restrict__ gate, uint32_t rows, uint32_t row, uint32_t pos, float eps, float ifreq) {
+    typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+    const int lane = threadIdx.x & 63, h0 = 4 * (threadIdx.x >> 6);
+    const Rope4 r = rope_angles(pos + row, lane, ifreq);
+    const float *src = qkv + (size_t)row * 8192 + h0 * 512 + 4 * lane;
+    float4 x[4], gv[4];
+#pragma unroll
+    for (int h = 0; h < 4; h++) {
+        x[h] = *reinterpret_cast<const float4 *>(src + h * 512);
+        gv[h] = *reinterpret_cast<const float4 *>(src + h * 512 + 256);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int h = h0 + i;
+        const float4 z = rope4(rms_norm4(x[i], eps, qw, lane, 1.0f), lane, r);
+        const half4 hz = {(_Float16)z.x, (_Float16)z.y, (_Float16)z.z, (_Float16)z.w};
+        *reinterpret_cast<half4 *>(packed + (((size_t)(h / 8) * rows + row) * 8 + h % 8) * 256 + 4 * lane) = hz;
+        *reinterpret_cast<float4 *>(gate + ((size_t)row * 16 + h) * 256 + 4 * lane) = gv[i];
+    }
+}
+
 __global__ __launch_bounds__(256) void prepare_fused_int8_kernel(
     const float *__restrict__ qkv, const float *__restrict__ k, const float *__restrict__ v,
     const uint16_t *__restrict__ qw, const uint16_t *__restrict__ kw, _Float16 *__restrict__ packed,
@@ -256,21 +283,7 @@ __global__ __launch_bounds__(256) void prepare_fused_int8_kernel(
     __shared__ __attribute__((aligned(16))) uint8_t vt[256 * vt_stride<kTile>()];
     const float ifreq = lane_inv_freq(theta);
     if (blockIdx.x < qblocks) {
-        const int lane = threadIdx.x & 63;
-        const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
-        if (row >= rows) return;                                     // wave-uniform
-        const Rope4 r = rope_angles(pos + row, lane, ifreq);
-        typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-#pragma unroll 4
-        for (int h = 0; h < 16; h++) {
-            const float *src = qkv + (size_t)row * 8192 + h * 512 + 4 * lane;
-            const float4 x = *reinterpret_cast<const float4 *>(src);
-            const float4 gv = *reinterpret_cast<const float4 *>(src + 256);
-            const float4 z = rope4(rms_norm4(x, eps, qw, lane, 1.0f), lane, r);
-            const half4 hz = {(_Float16)z.x, (_Float16)z.y, (_Float16)z.z, (_Float16)z.w};
-            *reinterpret_cast<half4 *>(packed + (((size_t)(h / 8) * rows + row) * 8 + h % 8) * 256 + 4 * lane) = hz;
-            *reinterpret_cast<float4 *>(gate + ((size_t)row * 16 + h) * 256 + 4 * lane) = gv;
-        }
+        prepare_query_heads(qkv, qw, packed, gate, rows, blockIdx.x, pos, eps, ifreq);
         return;
     }
     const uint32_t b = blockIdx.x - qblocks;
@@ -280,6 +293,38 @@ __global__ __launch_bounds__(256) void prepare_fused_int8_kernel(
 // batch_rope with FP16 KV storage (flags bit 256; kernels.metal:16-21, 322-324):
 // rotated Q in FP32, rotated K and V rounded to FP16 into the token-major
 // [cap][2][256] control cache. One wave per row; angles computed once per row.
+// FP16-KV fused preparation (attention_prepare_fused, kernels.metal:1889-1901): per token row,
+// the 16 query heads RMS-normalized with (w + 1), rotated, packed as grouped FP16 with the gate
+// split out (as prepare_fused_int8_kernel), and the 2 K heads normalized, rotated and stored with
+// V as FP16, token-major [pos + row][2][256] (kernels.metal:16-21). One wave per row.
+__global__ __launch_bounds__(256) void prepare_fused_half_kernel(
+    const float *__restrict__ qkv, const float *__restrict__ k, const float *__restrict__ v,
+    const uint16_t *__restrict__ qw, const uint16_t *__restrict__ kw, _Float16 *__restrict__ packed,
+    float *__restrict__ gate, _Float16 *__restrict__ kc, _Float16 *__restrict__ vc, uint32_t rows, uint32_t pos,
+    float theta, float eps) {
+    const float ifreq = lane_inv_freq(theta);
+    if (blockIdx.x < rows) {
+        prepare_query_heads(qkv, qw, packed, gate, rows, blockIdx.x, pos, eps, ifreq);
+        return;
+    }
+    // K/V: one wave per row
+    const int lane = threadIdx.x & 63;
+    const uint32_t row = (blockIdx.x - rows) * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;                                         // wave-uniform
+    const Rope4 r = rope_angles(pos + row, lane, ifreq);
+    typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const size_t src = (size_t)row * 512 + h * 256 + 4 * lane, dst = ((size_t)(pos + row) * 2 + h) * 256 + 4 * lane;
+        const float4 kz = rope4(rms_norm4(*reinterpret_cast<const float4 *>(k + src), eps, kw, lane, 1.0f), lane, r);
+        const float4 vz = *reinterpret_cast<const float4 *>(v + src);
+        const half4 kh = {(_Float16)kz.x, (_Float16)kz.y, (_Float16)kz.z, (_Float16)kz.w};
+        const half4 vh = {(_Float16)vz.x, (_Float16)vz.y, (_Float16)vz.z, (_Float16)vz.w};
+        *reinterpret_cast<half4 *>(kc + dst) = kh;
+        *reinterpret_cast<half4 *>(vc + dst) = vh;
+    }
+}
+
 __global__ __launch_bounds__(256) void batch_rope_half_kernel(const float *__restrict__ q, const float *__restrict__ k,
                                                               const float *__restrict__ v, float *__restrict__ qr,
                                                               _Float16 *__restrict__ kc, _Float16 *__restrict__ vc,
@@ -415,7 +460,7 @@ const char *launch_batch_rope_int8(Context &c, const View *b, int count, const b
     BOOT_REQUIRE(aligned(b[0].ptr, 16) && aligned(b[1].ptr, 16) && aligned(b[2].ptr, 16) && aligned(b[3].ptr, 16),
                  "Q/K/V bindings must be 16-byte aligned");
     if (const char *e = check_cache(b, 4, 5, 6, 7, end)) return e;
-    const uint32_t qblocks = (uint32_t)((rows + 3) / 4);
+    const uint32_t qblocks = (uint32_t)rows;   // one work-group per row for the query heads
     const uint32_t first = p.pos / kTile, last = (uint32_t)((end - 1) / kTile);
     const uint32_t blocks = qblocks + (last - first + 1) * 2;
     launch_timed(c, "batch_rope_int8_kernel", batch_rope_int8_kernel, dim3(blocks), dim3(256), 
@@ -456,12 +501,35 @@ const char *launch_prepare_fused_int8(Context &c, const View *b, int count, cons
                      aligned(b[4].ptr, 8) && aligned(b[5].ptr, 8) && aligned(b[6].ptr, 16),
                  "bindings misaligned");
     if (const char *e = check_cache(b, 7, 8, 9, 10, end)) return e;
-    const uint32_t qblocks = (uint32_t)((rows + 3) / 4);
+    const uint32_t qblocks = (uint32_t)rows;   // one work-group per row for the query heads
     const uint32_t first = p.pos / kTile, last = (uint32_t)((end - 1) / kTile);
     launch_timed(c, "prepare_fused_int8_kernel", prepare_fused_int8_kernel, dim3(qblocks + (last - first + 1) * 2), dim3(256), 
         (const float *)b[0].ptr, (const float *)b[1].ptr, (const float *)b[2].ptr, (const uint16_t *)b[3].ptr,
         (const uint16_t *)b[4].ptr, (_Float16 *)b[5].ptr, (float *)b[6].ptr, (int8_t *)b[7].ptr, (int8_t *)b[8].ptr,
         (float *)b[9].ptr, (float *)b[10].ptr, (uint32_t)rows, p.pos, p.theta, p.eps, qblocks, first);
+    return nullptr;
+}
+
+const char *launch_prepare_fused_half(Context &c, const View *b, int count, const boot_kernel_args &p,
+                                      const uint32_t *) {
+    // bindings (Prefill.cs:252): qkv, k, v, q_norm w, k_norm w, packed Q, gate, kc, vc (FP16 [cap][2][256])
+    BOOT_REQUIRE(count >= 9, "attention_prepare_fused needs 9 bindings");
+    const uint64_t rows = p.m, end = (uint64_t)p.pos + rows;
+    if (rows == 0) return nullptr;
+    BOOT_REQUIRE(b[0].bytes >= rows * 32768, "qkv input smaller than rows*8192 floats");
+    BOOT_REQUIRE(b[1].bytes >= rows * 2048 && b[2].bytes >= rows * 2048, "K/V input smaller than rows*512 floats");
+    BOOT_REQUIRE(b[3].bytes >= 512 && b[4].bytes >= 512, "norm weights smaller than 256 bf16");
+    BOOT_REQUIRE(b[5].bytes >= rows * 8192, "packed query smaller than rows*4096 halves");
+    BOOT_REQUIRE(b[6].bytes >= rows * 16384, "gate output smaller than rows*4096 floats");
+    BOOT_REQUIRE(b[7].bytes >= end * 1024 && b[8].bytes >= end * 1024, "FP16 KV cache smaller than position+rows");
+    BOOT_REQUIRE(aligned(b[0].ptr, 16) && aligned(b[1].ptr, 16) && aligned(b[2].ptr, 16) && aligned(b[3].ptr, 8) &&
+                     aligned(b[4].ptr, 8) && aligned(b[5].ptr, 8) && aligned(b[6].ptr, 16) && aligned(b[7].ptr, 8) &&
+                     aligned(b[8].ptr, 8),
+                 "bindings misaligned");
+    launch_timed(c, "prepare_fused_half_kernel", prepare_fused_half_kernel, dim3((uint32_t)(rows + (rows + 3) / 4)), dim3(256),
+        (const float *)b[0].ptr, (const float *)b[1].ptr, (const float *)b[2].ptr, (const uint16_t *)b[3].ptr,
+        (const uint16_t *)b[4].ptr, (_Float16 *)b[5].ptr, (float *)b[6].ptr, (_Float16 *)b[7].ptr,
+        (_Float16 *)b[8].ptr, (uint32_t)rows, p.pos, p.theta, p.eps);
     return nullptr;
 }
 

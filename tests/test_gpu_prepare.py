@@ -103,3 +103,39 @@ def test_fused_matches_fp64(device, oracle):
             assert vs[dest] == sv
     for buf in [rawb, kb, vb, qwb, kwb, packed, gate, *cache]:
         buf.dispose()
+
+
+def test_fused_fp16_equals_unfused_bitwise(device, oracle):
+    """FP16-KV fused preparation (attention_prepare_fused, kernels.metal:1889-1901) against the
+    unfused FP16 chain batch_split_q -> rmsnorm -> batch_rope (flags 256) ->
+    attention_query_grouped_half: packed query, gate and the FP16 K/V cache bitwise equal, and the
+    cache outside the appended rows untouched."""
+    raw, k, v, qw, kw = inputs(oracle)
+    p = KernelArgs(M=ROWS, Position=POSITION, K=LENGTH, Theta=10_000_000.0, Epsilon=1e-6, A=8, Flags=256)
+    rawb, kb, vb, qwb, kwb = (upload(device, a) for a in (raw, k, v, qw, kw))
+    guard = np.full((LENGTH + 1) * 512, 0x5555, np.uint16)
+    fused_k, fused_v, ref_k, ref_v = (upload(device, guard) for _ in range(4))
+    packed, packed_ref = device.allocate(ROWS * 8192), device.allocate(ROWS * 8192)
+    gate, gate_ref = device.allocate(ROWS * 16384), device.allocate(ROWS * 16384)
+    split, norm_k, rotated = device.allocate(ROWS * 16384), device.allocate(ROWS * 2048), device.allocate(ROWS * 16384)
+    dummy = device.allocate(4)
+    device.begin()
+    device.dispatch("batch_split_q", p, ROWS * 4096, 128, rawb, split, gate_ref)
+    device.dispatch("rmsnorm", KernelArgs(N=256, M=ROWS * 16, Flags=1, Epsilon=1e-6), ROWS * 16 * 256, 256,
+                    split, qwb, split, dummy)
+    device.dispatch("rmsnorm", KernelArgs(N=256, M=ROWS * 2, Flags=1, Epsilon=1e-6), ROWS * 2 * 256, 256,
+                    kb, kwb, norm_k, dummy)
+    device.dispatch("batch_rope", p, ROWS * 4096, 128, split, norm_k, vb, rotated, ref_k, ref_v)
+    device.dispatch("attention_query_grouped_half", p, ROWS * 1024, 128, rotated, packed_ref)
+    device.dispatch("attention_prepare_fused", p, ROWS * 18 * 256, 256, rawb, kb, vb, qwb, kwb, packed, gate,
+                    fused_k, fused_v)
+    device.end()
+    assert packed.read(np.uint8, ROWS * 8192).tobytes() == packed_ref.read(np.uint8, ROWS * 8192).tobytes()
+    assert gate.read(np.uint8, ROWS * 16384).tobytes() == gate_ref.read(np.uint8, ROWS * 16384).tobytes()
+    for a, b in ((fused_k, ref_k), (fused_v, ref_v)):
+        got = a.read(np.uint16, guard.size)
+        assert got.tobytes() == b.read(np.uint16, guard.size).tobytes()
+        assert np.all(got[:POSITION * 512] == 0x5555) and np.all(got[LENGTH * 512:] == 0x5555)
+    for buf in [rawb, kb, vb, qwb, kwb, fused_k, fused_v, ref_k, ref_v, packed, packed_ref, gate, gate_ref, split,
+                norm_k, rotated, dummy]:
+        buf.dispose()
