@@ -12,7 +12,8 @@ Metric: "30K-prefill INT8-KV attn ms/layer (MFMA %); 128K decode
   16 Q / 2 KV heads, d = 256.
 * decode (extra keys): config 4 — cache grown from 4096 tokens by doubling with device
   copies while being filled to 131072 tokens, pre-grown to 262144, then 256 sequential
-  single-token steps (batch_rope_int8 append + attention_decode_int8) over L = 131073..131328.
+  single-token steps over L = 131073..131328, each one attention_decode_append_int8 dispatch
+  per layer (batch_rope_int8 with M = 1 and the attention, fused; + split combine).
 * roofline: prefill attention kernel against the dense FP16 MFMA peak (2.5 PFLOP/s),
   decode kernel against HBM (8 TB/s); kernel durations from HIP events on the library's
   stream over the timed region.
@@ -323,10 +324,9 @@ class DecodeWorkload:
         for i in range(self.steps):
             pos = self.pos0 + i
             for layer in self.cache.layers:
-                engine.append_rows(d, layer, self.q.at(i * 16384), self.k_new.at(i * 2048), self.v_new.at(i * 2048),
-                                   self.rotated.at(i * 16384), 1, pos)
-                engine.decode(d, layer, self.rotated.at(i * 16384), self.gate.at(i * 16384), self.out.at(i * 16384),
-                              pos)
+                # batch_rope_int8 (M = 1) + attention over keys 0..pos, in one dispatch
+                engine.decode_append(d, layer, self.q.at(i * 16384), self.k_new.at(i * 2048), self.v_new.at(i * 2048),
+                                     self.rotated.at(i * 16384), self.gate.at(i * 16384), self.out.at(i * 16384), pos)
         d.end()
 
     def bulk_append(self):
@@ -440,11 +440,10 @@ def main():
     if dec is not None:
         device.reset_wall_timing(kernels_exact=True)
         dec.run()
-        kd = kernel_stats(device, ["decode_int8_kernel", "decode_combine_kernel", "batch_rope_int8_kernel"])
+        kd = kernel_stats(device, ["decode_int8_kernel", "decode_combine_kernel"])
         dispatches = dec.steps * len(dec.cache.layers)
         dec_kernel_ms = kd["decode_int8_kernel"][0] / dispatches
         dec_comb_ms = kd.get("decode_combine_kernel", (0.0, 0))[0] / dispatches
-        append_ms = kd["batch_rope_int8_kernel"][0] / dispatches
         bytes_per_dispatch = dec.kv_bytes() / dispatches
         device.reset_wall_timing(kernels_exact=True)
         dec.bulk_append()
@@ -455,7 +454,8 @@ def main():
             "kv_read_gbs_step": round(dec.kv_bytes() / dec.steps / (dec_wall * 1e-3) / 1e9, 1),
             "kv_read_gbs_attention_kernels": round(bytes_per_dispatch / ((dec_kernel_ms + dec_comb_ms) * 1e-3) / 1e9, 1),
             "ms_per_token_step_wall": round(dec_wall, 5), "decode_kernel_us": round(dec_kernel_ms * 1000, 3),
-            "combine_kernel_us": round(dec_comb_ms * 1000, 3), "append_kernel_us": round(append_ms * 1000, 3),
+            "combine_kernel_us": round(dec_comb_ms * 1000, 3),
+            "append": "fused into decode_int8_kernel (attention_decode_append_int8)",
             "bytes_per_layer_step": bytes_per_dispatch,
         }
         result["roofline_decode"] = {

@@ -407,6 +407,17 @@ def decode(device: Device, layer: Int8KvLayer, rotated, gate, output, position: 
                     gate, output, layer.key_scale, layer.value_scale)
 
 
+def decode_append(device: Device, layer: Int8KvLayer, q, k, v, rotated, gate, output, position: int,
+                  theta: float = ROPE_THETA) -> None:
+    """One decode step of QwenEngine.cs:161-165 in one dispatch: batch_rope_int8 with M = 1
+    (rotate q into ``rotated``, rotate k and append k/v at ``position``) followed by attention
+    of the rotated query over keys [0, position]. Same bytes as ``append_rows`` then ``decode``.
+    Inside a command."""
+    p = KernelArgs(M=1, K=position + 1, Position=position, Theta=theta)
+    device.dispatch("attention_decode_append_int8", p, 4096, 256, q, k, v, rotated, layer.key, layer.value,
+                    layer.key_scale, layer.value_scale, gate, output)
+
+
 def decode_reference_path(device: Device, layer: Int8KvLayer, rotated, gate, output, scores: GpuBuffer,
                           position: int, rows: int = 1) -> None:
     """The engine's three-kernel INT8 reader (QwenEngine.cs:163-165, Prefill.cs:280-283)."""

@@ -19,6 +19,7 @@
 //     P = p * vs[t]).
 #include "common.h"
 #include <type_traits>
+#include "kvmath.h"
 #include "mfma.h"
 
 namespace boot {
@@ -140,6 +141,15 @@ struct DecodeParams {
     float *partial;
     uint32_t rows, pos, splits;
     uint32_t split_chunks;   // 128-token chunks per split
+    // attention_decode_append_int8 (one row): q is the unrotated query; the kernel rotates it
+    // (writing it to `rotated`), quantizes the new token's K (rotated) and V into the cache at
+    // `pos` (k_out, v_out, ks_out, vs_out alias k, v, ks, vs) and attends over it
+    uint32_t append;
+    RopeFreq freq;
+    const float *knew, *vnew;    // FP32 [2][256] each
+    float *rotated;              // FP32 [16][256]
+    int8_t *k_out, *v_out;
+    float *ks_out, *vs_out;
 };
 
 __device__ inline float sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }
@@ -252,6 +262,51 @@ __device__ __attribute__((always_inline)) inline void store_v(ChunkLds &b, const
     b.v[d + 192][vp] = r.v3;
 }
 
+// The appended token's bytes in a chunk's registers, just before they are staged: K row `tn` of
+// the chunk (held by the 16 threads with tid / 16 == tn % 32, piece tid % 16, in register
+// tn / 32) and byte tn % 16 of the 16-token segment tn / 16 of every V page row (threads with
+// tid % 8 == tn / 16, rows tid / 8 + 64 i). Whatever the loads returned for that position is
+// replaced by the freshly quantized codes.
+// (selections are made on 32-bit words with masks: a select between whole uint4 values became a
+// select between their addresses and sent the register sets to scratch)
+__device__ __attribute__((always_inline)) inline void take_if(uint4 &w, uint32_t keep, const uint4 &f) {
+    w.x = (w.x & keep) | (f.x & ~keep);
+    w.y = (w.y & keep) | (f.y & ~keep);
+    w.z = (w.z & keep) | (f.z & ~keep);
+    w.w = (w.w & keep) | (f.w & ~keep);
+}
+
+__device__ __attribute__((always_inline)) inline void patch_k(KRegs &r, int tid, int tn, const uint4 *fresh) {
+    if ((tid >> 4) != (tn & 31)) return;
+    const uint4 f = fresh[tid & 15];
+    const int i = tn >> 5;
+    take_if(r.k0, i == 0 ? 0u : ~0u, f);
+    take_if(r.k1, i == 1 ? 0u : ~0u, f);
+    take_if(r.k2, i == 2 ? 0u : ~0u, f);
+    take_if(r.k3, i == 3 ? 0u : ~0u, f);
+}
+
+__device__ __attribute__((always_inline)) inline uint4 patch_byte(uint4 w, int byte, uint32_t code) {
+    const uint32_t sh = 8 * (byte & 3), value = (code & 0xffu) << sh;
+    const int word = byte >> 2;
+    const uint32_t m0 = word == 0 ? 0xffu << sh : 0u, m1 = word == 1 ? 0xffu << sh : 0u;
+    const uint32_t m2 = word == 2 ? 0xffu << sh : 0u, m3 = word == 3 ? 0xffu << sh : 0u;
+    w.x = (w.x & ~m0) | (value & m0);
+    w.y = (w.y & ~m1) | (value & m1);
+    w.z = (w.z & ~m2) | (value & m2);
+    w.w = (w.w & ~m3) | (value & m3);
+    return w;
+}
+
+__device__ __attribute__((always_inline)) inline void patch_v(VRegs &r, int tid, int tn, const uint8_t *fresh) {
+    if ((tid & 7) != (tn >> 4)) return;
+    const int d = tid >> 3, byte = tn & 15;
+    r.v0 = patch_byte(r.v0, byte, fresh[d]);
+    r.v1 = patch_byte(r.v1, byte, fresh[d + 64]);
+    r.v2 = patch_byte(r.v2, byte, fresh[d + 128]);
+    r.v3 = patch_byte(r.v3, byte, fresh[d + 192]);
+}
+
 // Grid: (splits, 2 KV groups, rows), one 8-wave work-group per CU; a split is
 // split_chunks chunks of 128 tokens, chosen on the host so that the grid fits the
 // CUs in one round. The work-group streams its chunks through double-buffered LDS
@@ -274,6 +329,11 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
     __shared__ uint2 pshare[2][kDecodeWaves][64];   // each wave's P operands, by chunk parity
     __shared__ float kscale[kMaxSplitTokens], vscale[kMaxSplitTokens];
     __shared__ float red[kDecodeWaves], qmax[4][8];
+    // append mode: rotated dims 0..63 of the group's 8 query heads, and the new token's codes
+    // (K row, V column) and scales
+    __shared__ __attribute__((aligned(16))) float qrot0[8][64];
+    __shared__ __attribute__((aligned(16))) uint8_t fresh_k[256], fresh_v[256];
+    __shared__ float fresh_scale[2];
     // INT8 query operands [set][MFMA c][lane] (set 0: q1 | q2 columns, set 1: q3), built once
     // and read into registers before the chunk loop. They sit in the V half of chunk buffer
     // 1, which is first written in phase 1, after the barrier that ends phase 0: by then every
@@ -289,13 +349,18 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
     const uint32_t begin = split * split_tokens;
     const uint32_t end = min(length, begin + split_tokens);
     const uint32_t nchunks = end > begin ? (end - begin + kChunk - 1) / kChunk : 0;
+    // append mode: the split holding the new token (position pos) stages fresh codes for it
+    const bool owner = p.append && begin <= p.pos && p.pos < end;
+    const int e_new = owner ? (int)(p.pos - begin) : -1;          // split-local index
+    const int jn = owner ? e_new / kChunk : -1, tn = owner ? e_new % kChunk : 0;
 
     // ---- the small loads first (scales of the split, this wave's query chunk), then
     // the first two chunks: waits on the memory counter are in order, so the set-up
     // below never waits for the chunks
     // (a fixed count of loads, no branches: the counter waits below stay exact;
     // indices past the split repeat its last token, a cache hit)
-    const uint32_t last = (end > begin ? end : length) - 1;
+    uint32_t last = (end > begin ? end : length) - 1;
+    if (p.append && last == p.pos && p.pos > 0) last = p.pos - 1;   // its stored scales are stale
     float ksv[kMaxSplitTokens / 512], vsv[kMaxSplitTokens / 512];
 #pragma unroll
     for (int it = 0; it < kMaxSplitTokens / 512; it++) {
@@ -312,6 +377,13 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
 #pragma unroll
         for (int f = 0; f < 4; f++) x[f] = *reinterpret_cast<const float4 *>(qh + 4 * f);
     }
+    // append mode: head `wave` of the group in rope4's layout (dims 4 lane .. +3) and the new
+    // token's K and V of the group. Loaded in every mode and every wave (from the query itself
+    // when there is no new token): a fixed count of loads keeps the counter waits exact.
+    const float *knew = p.append ? p.knew : p.q, *vnew = p.append ? p.vnew : p.q;
+    const float4 rq = *reinterpret_cast<const float4 *>(p.q + ((size_t)row * 16 + g * 8 + wave) * 256 + 4 * lane);
+    const float4 nk = *reinterpret_cast<const float4 *>(knew + (size_t)g * 256 + 4 * lane);
+    const float4 nv = *reinterpret_cast<const float4 *>(vnew + (size_t)g * 256 + 4 * lane);
     // every wave's small loads enter the CU's memory pipeline before any chunk load
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();
@@ -323,18 +395,72 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
     load_k(kb, p, g, begin, 1, nchunks, length, tid);
     load_v(vb, p, g, begin, 1, nchunks, tid);
 
+    float vmax = 0.0f;
+    if (p.append) {
+        // the same rotation (and, for the new token, quantization) as batch_rope_int8
+        // (kv_store.hip), so the cache bytes and the rotated query match it bit for bit
+        const float ifreq = lane_inv_freq(p.freq);
+        const Rope4 r = rope_angles(p.pos, lane, ifreq);
+        const float4 z = rope4(rq, lane, r);
+        if (lane < 16) *reinterpret_cast<float4 *>(&qrot0[wave][4 * lane]) = z;
+        if (owner) {
+            *reinterpret_cast<float4 *>(p.rotated + ((size_t)g * 8 + wave) * 256 + 4 * lane) = z;
+            const uint64_t vector = (uint64_t)p.pos * 2 + g;
+            if (wave == 0) {
+                const float4 kz = rope4(nk, lane, r);
+                const float ka = wave_max(fmaxf(fmaxf(fabsf(kz.x), fabsf(kz.y)), fmaxf(fabsf(kz.z), fabsf(kz.w))));
+                const float kr127 = 127.0f / ka;
+                const uint32_t codes = pack4(quant_code(kz.x, ka, kr127), quant_code(kz.y, ka, kr127),
+                                             quant_code(kz.z, ka, kr127), quant_code(kz.w, ka, kr127));
+                *reinterpret_cast<uint32_t *>(p.k_out + vector * 256 + 4 * lane) = codes;
+                *reinterpret_cast<uint32_t *>(&fresh_k[4 * lane]) = codes;
+                if (lane == 0) {
+                    p.ks_out[vector] = ka / 127.0f;
+                    fresh_scale[0] = ka / 127.0f;
+                }
+            } else if (wave == 1) {
+                const float va = wave_max(fmaxf(fmaxf(fabsf(nv.x), fabsf(nv.y)), fmaxf(fabsf(nv.z), fabsf(nv.w))));
+                const float vr127 = 127.0f / va;
+                const float c[4] = {quant_code(nv.x, va, vr127), quant_code(nv.y, va, vr127),
+                                    quant_code(nv.z, va, vr127), quant_code(nv.w, va, vr127)};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint8_t b = (uint8_t)(int8_t)(int)c[i];
+                    p.v_out[value_index(vector, 4 * lane + i)] = (int8_t)b;
+                    fresh_v[4 * lane + i] = b;
+                }
+                if (lane == 0) {
+                    p.vs_out[vector] = va / 127.0f;
+                    fresh_scale[1] = va / 127.0f;
+                }
+                vmax = va / 127.0f;   // the new token joins the split's largest V scale
+            }
+        }
+    }
+
     // ---- scales of the split (this group) into LDS, vs_ref = their maximum; the
     // per-head maxima of the query chunks
-    float vmax = 0.0f;
 #pragma unroll
     for (int it = 0; it < kMaxSplitTokens / 512; it++) {
         const uint32_t e = tid + 512 * it;   // < kMaxSplitTokens; entries past the split are never read
-        // masked by a multiply, not a select: every load above stays unconditional
-        // (the clamped indices never reach a poisoned, non-finite tail scale)
-        const float inside = begin + e < end ? 1.0f : 0.0f;
-        kscale[e] = ksv[it] * (kLog2e / 16.0f) * inside;
-        vscale[e] = vsv[it] * inside;
-        vmax = fmaxf(vmax, vsv[it] * inside);
+        // entries past the split are zero (selected after the unconditional loads); in append
+        // mode the new token's entry is set from its fresh scales below
+        const bool inside = begin + e < end && (int)e != e_new;
+        kscale[e] = inside ? ksv[it] * (kLog2e / 16.0f) : 0.0f;
+        vscale[e] = inside ? vsv[it] : 0.0f;
+        vmax = fmaxf(vmax, inside ? vsv[it] : 0.0f);
+    }
+    if (p.append) {
+        __syncthreads();   // the rotated query dims and the fresh codes and scales are in LDS
+        if (chunk == 0) {
+            // dims 16 qq + [0, 16) of head n % 8: the rotated values
+#pragma unroll
+            for (int f = 0; f < 4; f++) x[f] = *reinterpret_cast<const float4 *>(&qrot0[head][16 * qq + 4 * f]);
+        }
+        if (tid == 0 && owner) {
+            kscale[e_new] = fresh_scale[0] * (kLog2e / 16.0f);
+            vscale[e_new] = fresh_scale[1];
+        }
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) vmax = fmaxf(vmax, __shfl_xor(vmax, o, 64));
@@ -380,6 +506,7 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
         }
     }
     // K of chunk 0 into buffer 0 and K of chunk 2 into the registers it leaves
+    if (jn == 0) patch_k(ka, tid, tn, reinterpret_cast<const uint4 *>(fresh_k));
     store_k(bufs[0], ka, tid);
     load_k(ka, p, g, begin, 2, nchunks, length, tid);
     __syncthreads();
@@ -499,8 +626,10 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
             probs(sc_prev, local0, m, total_prev, j & 1);
             if (qq == 0) chunk_top[j & 1][wave][n] = top;
         }
+        if ((int)j == jn) patch_v(rv, tid, tn, fresh_v);
         store_v(bufs[j & 1], rv, tid);
         if (load_v2) load_v(rv, p, g, begin, j + 2, nchunks, tid);
+        if ((int)j + 1 == jn) patch_k(rk, tid, tn, reinterpret_cast<const uint4 *>(fresh_k));
         if (store_knext) store_k(bufs[(j + 1) & 1], rk, tid);
         if (load_k3) load_k(rk, p, g, begin, j + 3, nchunks, length, tid);
         __syncthreads();
@@ -739,6 +868,78 @@ const char *launch_values_int8(Context &c, const View *b, int count, const boot_
     return nullptr;
 }
 
+namespace {
+
+// Split geometry shared by both decode entry points: whole 128-token chunks per split, chosen so
+// that the grid (splits x 2 groups x rows, one work-group per CU) fits the CUs in one round (a
+// second, nearly empty round would double the time), at most kMaxSplitTokens per split.
+const char *decode_launch(Context &c, DecodeParams &d, uint64_t rows, uint64_t length) {
+    const uint64_t total_chunks = (length + kChunk - 1) / kChunk;
+    const uint64_t slots = std::max<uint64_t>(1, (uint64_t)std::max(1, context_cus(c)) / (2 * rows));
+    uint64_t split_chunks = (total_chunks + slots - 1) / slots;
+    split_chunks = std::min<uint64_t>(split_chunks, (uint64_t)(kMaxSplitTokens / kChunk));
+    const uint64_t splits = (total_chunks + split_chunks - 1) / split_chunks;
+    BOOT_REQUIRE(splits <= kMaxDecodeSplits, "too many decode splits");
+    d.rows = (uint32_t)rows;
+    d.splits = (uint32_t)splits;
+    d.split_chunks = (uint32_t)split_chunks;
+    d.partial = nullptr;
+    if (splits > 1) {
+        d.partial = (float *)context_workspace(c, rows * 2 * splits * kPartialFloats * sizeof(float));
+        BOOT_REQUIRE(d.partial, "cannot allocate decode split workspace");
+    }
+    launch_timed(c, "decode_int8_kernel", decode_int8_kernel, dim3((uint32_t)splits, 2, (uint32_t)rows), dim3(512), d);
+    if (splits > 1) {
+        context_split(c, "attention_decode_int8.combine");
+        launch_timed(c, "decode_combine_kernel", decode_combine_kernel, dim3(4, 16, (uint32_t)rows), dim3(256), d.partial,
+                     d.gate, d.y, (uint32_t)splits);
+    }
+    return nullptr;
+}
+
+}  // namespace
+
+const char *launch_decode_append_int8(Context &c, const View *b, int count, const boot_kernel_args &p,
+                                      const uint32_t *) {
+    // bindings: q FP32 [1][16][256] (unrotated), k, v FP32 [1][2][256] (the new token, K
+    // unrotated), rotated FP32 [1][16][256] (out), kc, vc, ks, vs (the cache, appended at
+    // Position), gate, y. One decode step of QwenEngine.cs:161-165: batch_rope_int8 with M = 1
+    // followed by attention over keys 0..Position, in one dispatch.
+    BOOT_REQUIRE(count >= 10, "attention_decode_append_int8 needs 10 bindings: q, k, v, rotated, kc, vc, ks, vs, gate, y");
+    BOOT_REQUIRE(p.m == 1, "attention_decode_append_int8 serves one row (M = 1)");
+    const uint64_t length = (uint64_t)p.pos + 1;
+    BOOT_REQUIRE(length <= 262144, "attended length exceeds the 262144-token window");
+    BOOT_REQUIRE(b[0].bytes >= 16384 && b[3].bytes >= 16384, "query/rotated buffers smaller than 4096 floats");
+    BOOT_REQUIRE(b[1].bytes >= 2048 && b[2].bytes >= 2048, "K/V input smaller than 512 floats");
+    BOOT_REQUIRE(b[4].bytes >= length * 512, "K cache smaller than Position + 1 tokens");
+    BOOT_REQUIRE(b[5].bytes >= value_bytes(length), "V cache smaller than whole pages of Position + 1 tokens");
+    BOOT_REQUIRE(b[6].bytes >= length * 8 && b[7].bytes >= length * 8, "KV scale buffers smaller than Position + 1 tokens");
+    BOOT_REQUIRE(b[8].bytes >= 16384 && b[9].bytes >= 16384, "gate/output smaller than 4096 floats");
+    BOOT_REQUIRE(aligned(b[0].ptr, 16) && aligned(b[1].ptr, 16) && aligned(b[2].ptr, 16) && aligned(b[3].ptr, 16) &&
+                     aligned(b[4].ptr, 16) && aligned(b[5].ptr, 16) && aligned(b[6].ptr, 4) && aligned(b[7].ptr, 4) &&
+                     aligned(b[8].ptr, 4) && aligned(b[9].ptr, 4),
+                 "bindings misaligned (q, k, v, rotated, kc, vc need 16 bytes)");
+    DecodeParams d;
+    d.q = (const float *)b[0].ptr;
+    d.knew = (const float *)b[1].ptr;
+    d.vnew = (const float *)b[2].ptr;
+    d.rotated = (float *)b[3].ptr;
+    d.k = (const int8_t *)b[4].ptr;
+    d.v = (const int8_t *)b[5].ptr;
+    d.ks = (const float *)b[6].ptr;
+    d.vs = (const float *)b[7].ptr;
+    d.k_out = (int8_t *)b[4].ptr;
+    d.v_out = (int8_t *)b[5].ptr;
+    d.ks_out = (float *)b[6].ptr;
+    d.vs_out = (float *)b[7].ptr;
+    d.gate = (const float *)b[8].ptr;
+    d.y = (float *)b[9].ptr;
+    d.pos = p.pos;
+    d.append = 1;
+    d.freq = rope_frequencies(p.theta);
+    return decode_launch(c, d, 1, length);
+}
+
 const char *launch_decode_int8(Context &c, const View *b, int count, const boot_kernel_args &p, const uint32_t *) {
     // bindings (EncodeInt8 order, DeviceAttention.cs:69): q FP32 [rows][16][256] (rotated),
     // k, v, gate, y, ks, vs. Row r attends t <= pos + r.
@@ -756,15 +957,6 @@ const char *launch_decode_int8(Context &c, const View *b, int count, const boot_
     BOOT_REQUIRE(aligned(b[0].ptr, 16) && aligned(b[1].ptr, 16) && aligned(b[2].ptr, 16) && aligned(b[3].ptr, 4) &&
                      aligned(b[4].ptr, 4) && aligned(b[5].ptr, 4) && aligned(b[6].ptr, 4),
                  "bindings misaligned (q, k, v need 16 bytes)");
-    // Split length in 128-token chunks, chosen so that the grid (splits x 2 groups x
-    // rows, one work-group per CU) fits the CUs in one round: a second, nearly empty
-    // round would double the time. At most kMaxSplitTokens per split.
-    const uint64_t total_chunks = (length + kChunk - 1) / kChunk;
-    const uint64_t slots = std::max<uint64_t>(1, (uint64_t)std::max(1, context_cus(c)) / (2 * rows));
-    uint64_t split_chunks = (total_chunks + slots - 1) / slots;
-    split_chunks = std::min<uint64_t>(split_chunks, (uint64_t)(kMaxSplitTokens / kChunk));
-    const uint64_t splits = (total_chunks + split_chunks - 1) / split_chunks;
-    BOOT_REQUIRE(splits <= kMaxDecodeSplits, "too many decode splits");
     DecodeParams d;
     d.q = (const float *)b[0].ptr;
     d.k = (const int8_t *)b[1].ptr;
@@ -773,22 +965,14 @@ const char *launch_decode_int8(Context &c, const View *b, int count, const boot_
     d.y = (float *)b[4].ptr;
     d.ks = (const float *)b[5].ptr;
     d.vs = (const float *)b[6].ptr;
-    d.rows = (uint32_t)rows;
     d.pos = p.pos;
-    d.splits = (uint32_t)splits;
-    d.split_chunks = (uint32_t)split_chunks;
-    d.partial = nullptr;
-    if (splits > 1) {
-        d.partial = (float *)context_workspace(c, rows * 2 * splits * kPartialFloats * sizeof(float));
-        BOOT_REQUIRE(d.partial, "cannot allocate decode split workspace");
-    }
-    launch_timed(c, "decode_int8_kernel", decode_int8_kernel, dim3((uint32_t)splits, 2, (uint32_t)rows), dim3(512), d);
-    if (splits > 1) {
-        context_split(c, "attention_decode_int8.combine");
-        launch_timed(c, "decode_combine_kernel", decode_combine_kernel, dim3(4, 16, (uint32_t)rows), dim3(256), d.partial,
-                     d.gate, d.y, (uint32_t)splits);
-    }
-    return nullptr;
+    d.append = 0;
+    d.freq = RopeFreq{};
+    d.knew = d.vnew = nullptr;
+    d.rotated = nullptr;
+    d.k_out = d.v_out = nullptr;
+    d.ks_out = d.vs_out = nullptr;
+    return decode_launch(c, d, rows, length);
 }
 
 }  // namespace boot

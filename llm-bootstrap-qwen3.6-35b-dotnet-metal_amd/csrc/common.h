@@ -87,6 +87,7 @@ const char *launch_online_fp16(Context &, const View *, int, const boot_kernel_a
 const char *launch_batch_rope_half(Context &, const View *, int, const boot_kernel_args &, const uint32_t *);
 const char *launch_prepare_fused_half(Context &, const View *, int, const boot_kernel_args &, const uint32_t *);
 const char *launch_decode_int8(Context &, const View *, int, const boot_kernel_args &, const uint32_t *);
+const char *launch_decode_append_int8(Context &, const View *, int, const boot_kernel_args &, const uint32_t *);
 const char *launch_scores_int8(Context &, const View *, int, const boot_kernel_args &, const uint32_t *);
 const char *launch_softmax(Context &, const View *, int, const boot_kernel_args &, const uint32_t *);
 const char *launch_values_int8(Context &, const View *, int, const boot_kernel_args &, const uint32_t *);

@@ -14,6 +14,7 @@
 // +-127. The library is built without fast-math, with correctly rounded fp32
 // division, so these are the IEEE operations the reference specifies.
 #include "common.h"
+#include "kvmath.h"
 #include "mfma.h"
 
 namespace boot {
@@ -27,107 +28,7 @@ constexpr uint64_t kBulkRows = 4096;    // appends of at least this many rows us
 template <int Tile>
 constexpr int vt_stride() { return Tile + 4; }
 
-__device__ inline float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
 
-__device__ inline float quant_code(float x, float amax, float recip) {
-    // kernels.metal:140: clamp(rint(amax > 0 ? x * (127/amax) : 0), -127, 127)
-    float c = amax > 0.0f ? rintf(x * recip) : 0.0f;
-    return fminf(fmaxf(c, -127.0f), 127.0f);
-}
-
-__device__ inline uint32_t pack4(float a, float b, float c, float d) {
-    return (uint32_t)(uint8_t)(int8_t)(int)a | ((uint32_t)(uint8_t)(int8_t)(int)b << 8) |
-           ((uint32_t)(uint8_t)(int8_t)(int)c << 16) | ((uint32_t)(uint8_t)(int8_t)(int)d << 24);
-}
-
-// Rotation angles of one position for the four dims a lane holds (4*lane .. +3):
-// lane j < 32 evaluates cos/sin of position * theta^(-2j/64) once
-// (kernels.metal:122-125), and lanes fetch the pairs of their dims
-// (j = d % 32) by shuffle, so one sincos per pair serves every head. `ifreq` is
-// the lane's theta^(-2j/64) from lane_inv_freq.
-struct Rope4 {
-    float c[4], s[4];
-};
-
-__device__ inline Rope4 rope_angles(uint32_t position, int lane, float ifreq) {
-    float cj = 1.0f, sj = 0.0f;
-    if (lane < 32) {
-        const float angle = (float)position * ifreq;
-        sincosf(angle, &sj, &cj);
-    }
-    Rope4 r;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int j = (lane * 4 + i) & 31;
-        r.c[i] = __shfl(cj, j, 64);
-        r.s[i] = __shfl(sj, j, 64);
-    }
-    return r;
-}
-
-// Partial RoPE of the float4 a lane holds (dims 4*lane .. 4*lane+3) of one
-// 256-dim head vector; dims < 64 rotate in pairs (j, j+32). The pair partner
-// of lane l < 16 is lane l ^ 8. Every lane must call this (shuffles).
-__device__ inline float4 rope4(float4 x, int lane, const Rope4 &r) {
-    float4 p;
-    p.x = __shfl_xor(x.x, 8, 64);
-    p.y = __shfl_xor(x.y, 8, 64);
-    p.z = __shfl_xor(x.z, 8, 64);
-    p.w = __shfl_xor(x.w, 8, 64);
-    if (lane >= 16) return x;
-    float in[4] = {x.x, x.y, x.z, x.w}, partner[4] = {p.x, p.y, p.z, p.w}, out[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int d = lane * 4 + i;
-        if (d < 32) out[i] = fmaf(in[i], r.c[i], -(partner[i] * r.s[i]));   // a*cos - b*sin, b = x[j+32]
-        else out[i] = fmaf(in[i], r.c[i], partner[i] * r.s[i]);              // b*cos + a*sin, a = x[j]
-    }
-    return make_float4(out[0], out[1], out[2], out[3]);
-}
-
-// pow(theta, -float(2*j)/64.0f) as an fp32 value for lane j < 32 (kernels.metal:123):
-// evaluated in fp64 and rounded once, so it is the correctly rounded fp32 value of the
-// reference's expression (theta and the exponent are exact in fp32). One ulp of it moves
-// the angle at position 262143 by ~0.016 rad. Computed per wave in registers: no LDS
-// table and no barrier, so a kernel's loads go out first.
-__device__ inline float lane_inv_freq(float theta) {
-    const int j = threadIdx.x & 63;
-    return j < 32 ? (float)pow((double)theta, (double)(-(float)(2 * j) / 64.0f)) : 0.0f;
-}
-
-// RMS normalization of one 256-dim vector held as a float4 per lane, with the
-// weights (bf16 w + 1) of QwenEngine's q_norm/k_norm (kernels.metal:51-57 with
-// flag 1): y = x * (1/sqrt(mean(x^2) + eps)) * (w + 1). The sum of squares
-// has one fixed order (lane partial, then a butterfly), shared by rmsnorm and
-// the fused preparation so both give identical bits.
-__device__ inline float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-
-__device__ inline float bf16_to_float(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
-
-__device__ inline float4 rms_norm4(float4 x, float eps, const uint16_t *w, int lane, float offset) {
-    const float total = wave_sum(((x.x * x.x + x.y * x.y) + x.z * x.z) + x.w * x.w);
-    const float inv = 1.0f / sqrtf(total / 256.0f + eps);
-    const uint2 wb = *reinterpret_cast<const uint2 *>(w + 4 * lane);
-    float4 y;
-    y.x = x.x * inv * (bf16_to_float(wb.x & 0xffff) + offset);
-    y.y = x.y * inv * (bf16_to_float(wb.x >> 16) + offset);
-    y.z = x.z * inv * (bf16_to_float(wb.y & 0xffff) + offset);
-    y.w = x.w * inv * (bf16_to_float(wb.y >> 16) + offset);
-    return y;
-}
-
-struct KNorm {
-    const uint16_t *w;   // k_norm weights (bf16); null: no normalization
-    float eps;
-};
 
 // Quantizes and appends tokens [lo, hi) of one Tile-token tile for one KV head.
 // K: one wave per token, float4 per lane, codes written token-major as char4.
@@ -219,10 +120,10 @@ __global__ __launch_bounds__(256) void kv_store_int8_kernel(
 __global__ __launch_bounds__(256) void batch_rope_int8_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
     float *__restrict__ qr, int8_t *__restrict__ kc, int8_t *__restrict__ vc,
-    float *__restrict__ ks, float *__restrict__ vs, uint32_t rows, uint32_t pos, float theta,
+    float *__restrict__ ks, float *__restrict__ vs, uint32_t rows, uint32_t pos, RopeFreq freq,
     uint32_t qblocks, uint32_t first_tile) {
     __shared__ __attribute__((aligned(16))) uint8_t vt[256 * vt_stride<kTile>()];
-    const float ifreq = lane_inv_freq(theta);
+    const float ifreq = lane_inv_freq(freq);
     if (blockIdx.x < qblocks) {
         // one work-group per row, wave w rotating heads 4w..4w+3 (loads issued together)
         const int lane = threadIdx.x & 63, h0 = 4 * (threadIdx.x >> 6);
@@ -278,10 +179,10 @@ __global__ __launch_bounds__(256) void prepare_fused_int8_kernel(
     const float *__restrict__ qkv, const float *__restrict__ k, const float *__restrict__ v,
     const uint16_t *__restrict__ qw, const uint16_t *__restrict__ kw, _Float16 *__restrict__ packed,
     float *__restrict__ gate, int8_t *__restrict__ kc, int8_t *__restrict__ vc, float *__restrict__ ks,
-    float *__restrict__ vs, uint32_t rows, uint32_t pos, float theta, float eps, uint32_t qblocks,
+    float *__restrict__ vs, uint32_t rows, uint32_t pos, RopeFreq freq, float eps, uint32_t qblocks,
     uint32_t first_tile) {
     __shared__ __attribute__((aligned(16))) uint8_t vt[256 * vt_stride<kTile>()];
-    const float ifreq = lane_inv_freq(theta);
+    const float ifreq = lane_inv_freq(freq);
     if (blockIdx.x < qblocks) {
         prepare_query_heads(qkv, qw, packed, gate, rows, blockIdx.x, pos, eps, ifreq);
         return;
@@ -301,8 +202,8 @@ __global__ __launch_bounds__(256) void prepare_fused_half_kernel(
     const float *__restrict__ qkv, const float *__restrict__ k, const float *__restrict__ v,
     const uint16_t *__restrict__ qw, const uint16_t *__restrict__ kw, _Float16 *__restrict__ packed,
     float *__restrict__ gate, _Float16 *__restrict__ kc, _Float16 *__restrict__ vc, uint32_t rows, uint32_t pos,
-    float theta, float eps) {
-    const float ifreq = lane_inv_freq(theta);
+    RopeFreq freq, float eps) {
+    const float ifreq = lane_inv_freq(freq);
     if (blockIdx.x < rows) {
         prepare_query_heads(qkv, qw, packed, gate, rows, blockIdx.x, pos, eps, ifreq);
         return;
@@ -328,8 +229,8 @@ __global__ __launch_bounds__(256) void prepare_fused_half_kernel(
 __global__ __launch_bounds__(256) void batch_rope_half_kernel(const float *__restrict__ q, const float *__restrict__ k,
                                                               const float *__restrict__ v, float *__restrict__ qr,
                                                               _Float16 *__restrict__ kc, _Float16 *__restrict__ vc,
-                                                              uint32_t rows, uint32_t pos, float theta) {
-    const float ifreq = lane_inv_freq(theta);
+                                                              uint32_t rows, uint32_t pos, RopeFreq freq) {
+    const float ifreq = lane_inv_freq(freq);
     const int lane = threadIdx.x & 63;
     const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;                                         // wave-uniform
@@ -466,7 +367,7 @@ const char *launch_batch_rope_int8(Context &c, const View *b, int count, const b
     launch_timed(c, "batch_rope_int8_kernel", batch_rope_int8_kernel, dim3(blocks), dim3(256), 
         (const float *)b[0].ptr, (const float *)b[1].ptr, (const float *)b[2].ptr, (float *)b[3].ptr,
         (int8_t *)b[4].ptr, (int8_t *)b[5].ptr, (float *)b[6].ptr, (float *)b[7].ptr, (uint32_t)rows,
-        p.pos, p.theta, qblocks, first);
+        p.pos, rope_frequencies(p.theta), qblocks, first);
     return nullptr;
 }
 
@@ -506,7 +407,7 @@ const char *launch_prepare_fused_int8(Context &c, const View *b, int count, cons
     launch_timed(c, "prepare_fused_int8_kernel", prepare_fused_int8_kernel, dim3(qblocks + (last - first + 1) * 2), dim3(256), 
         (const float *)b[0].ptr, (const float *)b[1].ptr, (const float *)b[2].ptr, (const uint16_t *)b[3].ptr,
         (const uint16_t *)b[4].ptr, (_Float16 *)b[5].ptr, (float *)b[6].ptr, (int8_t *)b[7].ptr, (int8_t *)b[8].ptr,
-        (float *)b[9].ptr, (float *)b[10].ptr, (uint32_t)rows, p.pos, p.theta, p.eps, qblocks, first);
+        (float *)b[9].ptr, (float *)b[10].ptr, (uint32_t)rows, p.pos, rope_frequencies(p.theta), p.eps, qblocks, first);
     return nullptr;
 }
 
@@ -529,7 +430,7 @@ const char *launch_prepare_fused_half(Context &c, const View *b, int count, cons
     launch_timed(c, "prepare_fused_half_kernel", prepare_fused_half_kernel, dim3((uint32_t)(rows + (rows + 3) / 4)), dim3(256),
         (const float *)b[0].ptr, (const float *)b[1].ptr, (const float *)b[2].ptr, (const uint16_t *)b[3].ptr,
         (const uint16_t *)b[4].ptr, (_Float16 *)b[5].ptr, (float *)b[6].ptr, (_Float16 *)b[7].ptr,
-        (_Float16 *)b[8].ptr, (uint32_t)rows, p.pos, p.theta, p.eps);
+        (_Float16 *)b[8].ptr, (uint32_t)rows, p.pos, rope_frequencies(p.theta), p.eps);
     return nullptr;
 }
 
@@ -547,7 +448,7 @@ const char *launch_batch_rope_half(Context &c, const View *b, int count, const b
                  "bindings misaligned");
     launch_timed(c, "batch_rope_half_kernel", batch_rope_half_kernel, dim3((uint32_t)((rows + 3) / 4)), dim3(256), 
         (const float *)b[0].ptr, (const float *)b[1].ptr, (const float *)b[2].ptr, (float *)b[3].ptr,
-        (_Float16 *)b[4].ptr, (_Float16 *)b[5].ptr, (uint32_t)rows, p.pos, p.theta);
+        (_Float16 *)b[4].ptr, (_Float16 *)b[5].ptr, (uint32_t)rows, p.pos, rope_frequencies(p.theta));
     return nullptr;
 }
 

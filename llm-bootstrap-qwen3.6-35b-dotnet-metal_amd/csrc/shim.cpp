@@ -163,6 +163,7 @@ const std::unordered_map<std::string, Entry> &registry() {
         {"attention_online_int8", {launch_online_int8, 3}},
         {"attention_online_int8_q32_k128", {launch_online_int8, 3}},
         {"attention_decode_int8", {launch_decode_int8, 3}},
+        {"attention_decode_append_int8", {launch_decode_append_int8, 3}},
         {"attention_online_q32_k256_s8_g8_r2", {launch_online_fp16, 3}},
         {"batch_rope", {launch_batch_rope_half, -1}},
         {"attention_prepare_fused", {launch_prepare_fused_half, -1}},

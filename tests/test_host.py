@@ -120,3 +120,21 @@ def test_buffer_dispose_after_device_close_does_not_release():
     kept.dispose()                                       # after close: handle forgotten only
     assert device.lib.calls == [("release", 102), ("destroy", 7)]
     assert kept.handle == 0 and released.handle == 0
+
+
+def test_rope_frequencies_are_correctly_rounded():
+    """The launchers evaluate the RoPE frequencies pow(theta, -float(2j)/64) (kernels.metal:123)
+    as (float)pow((double)theta, ...) on the host; for the thetas in use that is the correctly
+    rounded FP32 value of the exact power (checked here with 60-digit decimal arithmetic)."""
+    import math
+    from decimal import Decimal, getcontext
+    import numpy as np
+    getcontext().prec = 60
+    for theta in (10_000_000.0, 1_000_000.0, 10_000.0):
+        for j in range(32):
+            exact = (Decimal(theta).ln() * (Decimal(-2 * j) / Decimal(64))).exp()
+            host = np.float32(math.pow(theta, float(np.float32(-(2 * j)) / np.float32(64.0))))
+            f = np.float32(float(exact))
+            nearest = min((np.nextafter(f, np.float32(-1)), f, np.nextafter(f, np.float32(2))),
+                          key=lambda c: abs(Decimal(float(c)) - exact))
+            assert host == nearest, (theta, j)
