@@ -59,6 +59,11 @@ def upload(device, array):
     return b
 
 
+# the INT8 prefill attention kernel of the library's build: one wave per SIMD (default) or
+# the two-team work-group (built with -DBOOT_PREFILL_PP)
+PREFILL_INT8_KERNELS = ["prefill_w64_kernel", "prefill_pp_kernel"]
+
+
 def kernel_stats(device, names):
     stats = {k["kernel"]: k for k in device.read_wall_timing()["kernels"]}
     out = {}
@@ -400,10 +405,14 @@ def main():
     device.reset_wall_timing(kernels_exact=True)
     for _ in range(args.steps):
         work.step()
-    ks = kernel_stats(device, ["prefill_pp_kernel", "prefill_combine_half_kernel", "prepare_fused_int8_kernel"])
-    attn_ms = ks["prefill_pp_kernel"][0] / args.steps
+    timed = kernel_stats(device, PREFILL_INT8_KERNELS)
+    attn_kernel = next((k for k in PREFILL_INT8_KERNELS if k in timed), None)
+    if attn_kernel is None:
+        raise SystemExit("no INT8 prefill attention kernel was timed")
+    ks = kernel_stats(device, [attn_kernel, "prefill_combine_half_kernel", "prepare_fused_int8_kernel"])
+    attn_ms = ks[attn_kernel][0] / args.steps
     combine_ms = ks.get("prefill_combine_half_kernel", (0.0, 0))[0] / args.steps
-    launches = ks["prefill_pp_kernel"][1] // args.steps
+    launches = ks[attn_kernel][1] // args.steps
     flops = work.flops()
     achieved = flops / (attn_ms * 1e-3) / 1e12
     result = {
@@ -418,12 +427,12 @@ def main():
                     "prepare_ms_per_layer": round(ks["prepare_fused_int8_kernel"][0] / args.steps, 4),
                     "attention_launches_per_layer": launches,
                     "mfma_fraction_end_to_end": round(flops / (wall_ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4)},
-        "roofline": {"bound": "mfma", "kernel": "prefill_pp_kernel (attention_online_int8_q32_k256_r2)",
+        "roofline": {"bound": "mfma", "kernel": f"{attn_kernel} (attention_online_int8_q32_k256_r2)",
                      "achieved": round(achieved, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / MFMA_PEAK_TFLOPS, 4),
-                     "traffic": measured_traffic("prefill_pp_kernel"),
-                     "mfma_busy": (measured_counters("prefill_pp_kernel") or {}).get("mfma_busy"),
-                     "counters": measured_counters("prefill_pp_kernel"),
+                     "traffic": measured_traffic(attn_kernel),
+                     "mfma_busy": (measured_counters(attn_kernel) or {}).get("mfma_busy"),
+                     "counters": measured_counters(attn_kernel),
                      "flops_per_layer": flops},
     }
     device.reset_wall_timing(kernels_exact=True)

@@ -31,6 +31,7 @@
 // (m, l, O); blocks sharing a key range are placed on the same XCD so its L2
 // serves their K/V tiles.
 #include "common.h"
+#include <type_traits>
 #include "mfma.h"
 
 namespace boot {
@@ -307,6 +308,24 @@ __device__ inline float max3f(float a, float b, float c) {
     float r;
     asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
     return r;
+}
+
+// S += A B^T with the accumulators in architectural VGPRs. At one wave per SIMD the compiler
+// gives every MFMA of a kernel the accumulator-register form; where O already fills the 256
+// accumulator registers, these keep S out of them. Dependent MFMAs of one chain (srcC exactly
+// the previous destination, same opcode) need no wait states; the chain's last MFMA is followed
+// by 24, which cover vector reads and writes of S after it (the 8-pass XDL RAW/WAW/WAR windows).
+// The operands come from LDS or global loads (no VALU write precedes an MFMA read).
+__device__ __forceinline__ void s_mfma_first(floatx16 &s, const half8 &a, const half8 &b) {
+    asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, 0" : "=&v"(s) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void s_mfma(floatx16 &s, const half8 &a, const half8 &b) {
+    asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+v"(s) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void s_mfma_last(floatx16 &s, const half8 &a, const half8 &b) {
+    asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
+                 : "+v"(s)
+                 : "v"(a), "v"(b));
 }
 
 struct PPTile {
@@ -664,6 +683,476 @@ __global__ __launch_bounds__(512, 1) void prefill_pp_kernel(PrefillParams p) {
     }
 }
 
+// ---------------------------------------------------------------- INT8 prefill, one wave per SIMD
+//
+// A work-group of 4 waves (one per SIMD, up to 512 registers each) owns 256 logical rows of one
+// KV group, as prefill_pp_kernel; wave w owns rows 64w .. 64w + 63 as two 32-row blocks, so every
+// K or V operand read from LDS feeds two MFMAs, its query stays in registers and its O^T
+// accumulators fill the accumulator registers. A single wave overlaps its own VALU work with its
+// MFMAs: an MFMA occupies the matrix pipe for ~32 cycles while the wave issues independent VALU
+// instructions beside it (about six per MFMA come free). Each 32-key tile n runs in two phases:
+//   A: S(n) = K(n) Q^T for both row blocks (32 MFMAs), interleaved with the INT8 -> FP16 staging
+//      of tile n + 1 and the loads of tile n + 2;
+//   B: O += V(n - 1)^T P(n - 1) for both row blocks (32 MFMAs), interleaved with the online
+//      softmax of S(n), which produces P(n).
+// One work-group barrier per tile, between the phases. K tiles are double-buffered and V tiles
+// (with the tile's scales) quadruple-buffered, so that a buffer written in phase A of tile n
+// was last read before the barrier of tile n - 1 and the operand reads of the next phase never
+// wait for a barrier: tile n + 1's K operands are read ahead during phase B of tile n.
+constexpr int kW64Keys = 32;               // keys per tile
+constexpr int kW64VBufs = 4;               // V^T tiles in LDS
+#ifndef BOOT_W64_QLDS
+#define BOOT_W64_QLDS 5
+#endif
+constexpr int kW64QLds = BOOT_W64_QLDS;    // Q^T chunks per row block kept in LDS, the rest in registers
+constexpr int kW64QRegs = 16 - kW64QLds;
+
+struct W64KTile {
+    _Float16 k[kW64Keys * kKStride];       // K codes as FP16, key-major (528-byte rows)
+};
+struct W64VTile {
+    _Float16 v[256 * kW64Keys];            // V^T codes as FP16: 64-byte dimension rows whose 16-byte
+                                           // pieces are XOR-swizzled by (row / 4) % 4
+    float ks[kW64Keys];                    // K scale * log2(e) / 16 (0 beyond K)
+    float vs[kW64Keys];                    // V scale / vs_ref (0 beyond K)
+};
+
+__global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
+    __shared__ W64KTile kbuf[2];
+    __shared__ W64VTile vbuf[kW64VBufs];
+    __shared__ uint4 qlds[kW64QLds > 0 ? kW64QLds : 1][2][256];   // [chunk][row block][thread]
+    __shared__ float vs_partial[4];
+
+    uint32_t g, tile, split;
+    {
+        const uint32_t b = blockIdx.x;
+        uint32_t combo;
+        if (p.remap) {
+            const uint32_t xcd = b % 8, idx = b / 8;
+            combo = xcd + 8 * (idx / p.tiles);
+            tile = idx % p.tiles;
+        } else {
+            combo = b / p.tiles;
+            tile = b % p.tiles;
+        }
+        g = combo % 2;
+        split = combo / 2;
+    }
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: wave-level branches stay scalar
+    const int i = lane & 31, kk = lane >> 5;
+    const uint32_t R = p.rows * 8;
+    const uint32_t r0 = tile * kPPRows + 64 * wave;          // first row of this wave
+    uint32_t my_row[2], limit[2];
+    bool row_valid[2];
+#pragma unroll
+    for (int rb = 0; rb < 2; rb++) {
+        my_row[rb] = r0 + 32 * rb + i;
+        row_valid[rb] = my_row[rb] < R;
+        limit[rb] = p.pos + (row_valid[rb] ? my_row[rb] : R - 1) / 8;   // keys <= limit visible
+    }
+    const uint32_t tile_last = min(R - 1, tile * kPPRows + kPPRows - 1);
+    const uint32_t tile_end = p.pos + tile_last / 8 + 1;               // keys [0, tile_end)
+    const uint32_t kbeg = split * p.split_keys;
+    const uint32_t kend = min(tile_end, kbeg + p.split_keys);
+    const int ntiles = kend > kbeg ? (int)((kend - kbeg + kW64Keys - 1) / kW64Keys) : 0;
+    const uint32_t wave_min_limit = p.pos + min(R - 1, r0) / 8;
+    const uint32_t last_key0 = kbeg + (uint32_t)max(ntiles - 1, 0) * kW64Keys;   // loads never go past it
+
+    // ---- staging: thread t converts 32 K codes (rows krow0 and krow0 + 4, 16 codes at
+    // 16 * kchunk; a load instruction reads four whole 256-byte rows) and the 32 V codes of
+    // page row t; threads t < 32 carry the scales of key t
+    const int8_t *kcodes = (const int8_t *)p.k;
+    const int8_t *vcodes = (const int8_t *)p.v;
+    const int krow0 = 8 * wave + (lane >> 4), kchunk = lane & 15;
+    uint4 rk0, rk1, rv0, rv1;
+    float pre_ks = 0.0f, pre_vs = 0.0f;
+    auto load_raw = [&](uint32_t key0) __attribute__((always_inline)) {
+        key0 = min(key0, last_key0);
+        const uint32_t ka = min(key0 + (uint32_t)krow0, p.keys - 1), kb2 = min(key0 + (uint32_t)krow0 + 4, p.keys - 1);
+        rk0 = *reinterpret_cast<const uint4 *>(kcodes + (size_t)((ka * 2 + g) * 256 + kchunk * 16));
+        rk1 = *reinterpret_cast<const uint4 *>(kcodes + (size_t)((kb2 * 2 + g) * 256 + kchunk * 16));
+        const size_t offv = (size_t)value_index((uint64_t)key0 * 2 + g, 0) + (size_t)tid * 256;
+        rv0 = *reinterpret_cast<const uint4 *>(vcodes + offv);
+        rv1 = *reinterpret_cast<const uint4 *>(vcodes + offv + 16);
+        const size_t at = (size_t)min(key0 + (uint32_t)(tid & 31), p.keys - 1) * 2 + g;
+        pre_ks = p.ks[at];
+        pre_vs = p.vs[at];
+    };
+    float vs_inv = 0.0f;
+    // Staging in pieces, so that phase A can spread them between its MFMAs. Piece j < 4 converts
+    // and writes 8 K codes, piece 4 <= j < 8 8 V codes; every wave writes the tile's scales (the
+    // same values from each wave: lane l carries key l % 32).
+    const int vsw_stage = (tid >> 2) & 3;
+    auto stage_piece = [&](W64KTile &kb, W64VTile &vb, int j) __attribute__((always_inline)) {
+        const uint4 &r = j < 2 ? rk0 : j < 4 ? rk1 : j < 6 ? rv0 : rv1;
+        const uint32_t lo = (j & 1) ? r.z : r.x, hi = (j & 1) ? r.w : r.y;
+        uint4 h;
+        i8x4_to_f16(lo, h.x, h.y);
+        i8x4_to_f16(hi, h.z, h.w);
+        if (j < 4)
+            *reinterpret_cast<uint4 *>(kb.k + (krow0 + 4 * (j >> 1)) * kKStride + kchunk * 16 + 8 * (j & 1)) = h;
+        else
+            *reinterpret_cast<uint4 *>(vb.v + tid * kW64Keys + 8 * ((j - 4) ^ vsw_stage)) = h;
+    };
+    auto stage_scales = [&](W64VTile &vb, uint32_t key0) __attribute__((always_inline)) {
+        const int t = tid & 31;
+        const bool inside = key0 + t < p.keys;   // poisoned tails beyond K never reach S or P
+        vb.ks[t] = inside ? pre_ks * (kLog2e / 16.0f) : 0.0f;
+        vb.vs[t] = inside ? pre_vs * vs_inv : 0.0f;
+    };
+    auto stage = [&](W64KTile &kb, W64VTile &vb, uint32_t key0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) stage_piece(kb, vb, j);
+        stage_scales(vb, key0);
+    };
+
+    // ---- prologue: the V scales of the split (vs_ref), tile 0's codes, the query
+    float vsv[8];
+#pragma unroll
+    for (int it = 0; it < 8; it++) {
+        const uint32_t key = kbeg + tid + 256 * it;
+        vsv[it] = key < kend ? p.vs[(size_t)key * 2 + g] : 0.0f;
+    }
+    load_raw(kbeg);
+    half8 qop[2][kW64QRegs];
+#pragma unroll
+    for (int rb = 0; rb < 2; rb++) {
+        const uint32_t rr = row_valid[rb] ? my_row[rb] : R - 1;
+        const _Float16 *qrow = p.q + ((size_t)g * R + rr) * 256 + 8 * kk;
+#pragma unroll
+        for (int c = 0; c < kW64QRegs; c++) qop[rb][c] = *reinterpret_cast<const half8 *>(qrow + 16 * c);
+#pragma unroll
+        for (int c = kW64QRegs; c < 16; c++) qlds[c - kW64QRegs][rb][tid] = *reinterpret_cast<const uint4 *>(qrow + 16 * c);
+    }
+    float vs_ref = 0.0f;
+#pragma unroll
+    for (int it = 0; it < 8; it++) vs_ref = fmaxf(vs_ref, vsv[it]);
+    for (uint32_t key = kbeg + tid + 2048; key < kend; key += 256) vs_ref = fmaxf(vs_ref, p.vs[(size_t)key * 2 + g]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) vs_ref = fmaxf(vs_ref, __shfl_xor(vs_ref, o, 64));
+    if (lane == 0) vs_partial[wave] = vs_ref;
+    __syncthreads();
+    vs_ref = fmaxf(fmaxf(vs_partial[0], vs_partial[1]), fmaxf(vs_partial[2], vs_partial[3]));
+    vs_ref = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, vs_ref)));
+    vs_inv = __builtin_bit_cast(
+        float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, vs_ref > 0.0f ? 1.0f / vs_ref : 0.0f)));
+    stage(kbuf[0], vbuf[0], kbeg);
+    load_raw(kbeg + kW64Keys);
+    {
+        // the V^T tile that the PV of "tile -1" reads, with zero probabilities: zero, not NaN
+        uint4 *z = reinterpret_cast<uint4 *>(vbuf[kW64VBufs - 1].v);
+        for (int e = tid; e < 256 * kW64Keys * 2 / 16; e += 256) z[e] = make_uint4(0, 0, 0, 0);
+    }
+    __syncthreads();
+
+    floatx16 o[2][8];
+#pragma unroll
+    for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) o[rb][dt][v] = 0.0f;
+    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
+    half8 pb[2][2];          // P(n - 1): [row block][16-key step]
+#pragma unroll
+    for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) pb[rb][0][e] = pb[rb][1][e] = (_Float16)0.0f;
+    auto qop_at = [&](int rb, int c) __attribute__((always_inline)) {
+        return c < kW64QRegs ? qop[rb][c < kW64QRegs ? c : 0]
+                             : __builtin_bit_cast(half8, qlds[c < kW64QRegs ? 0 : c - kW64QRegs][rb][tid]);
+    };
+
+    // the K and V scales of tile n, as the softmax lanes use them
+    auto load_scales = [&](int n, float4 (&k4)[4], float4 (&v4)[4]) __attribute__((always_inline)) {
+        const W64VTile &sb = vbuf[n % kW64VBufs];
+#pragma unroll
+        for (int q4 = 0; q4 < 4; q4++) {
+            k4[q4] = *reinterpret_cast<const float4 *>(sb.ks + 16 * (q4 >> 1) + 8 * kk + 4 * (q4 & 1));
+            v4[q4] = *reinterpret_cast<const float4 *>(sb.vs + 16 * (q4 >> 1) + 8 * kk + 4 * (q4 & 1));
+        }
+    };
+
+    // Phase A of tile n: S(n) for both row blocks, K operands read three steps ahead; the staging
+    // of tile n + 1 and the loads of tile n + 2 are spread between the MFMAs.
+    auto phase_a = [&](int n, floatx16 (&sc)[2], float4 (&k4)[4], float4 (&v4)[4]) __attribute__((always_inline)) {
+        const _Float16 *kr = kbuf[n & 1].k + qk_key_row(i) * kKStride + 8 * kk;
+        const uint32_t next0 = kbeg + (uint32_t)(n + 1) * kW64Keys;
+        W64KTile &kdst = kbuf[(n + 1) & 1];                 // past the last tile: unread buffers
+        W64VTile &vdst = vbuf[(n + 1) % kW64VBufs];
+        half8 kop[4];                                       // K operands, read three steps ahead
+        half8 qop_l[4][2];                                  // Q^T chunks from LDS, likewise
+#pragma unroll
+        for (int c = 0; c < 3; c++) {
+            kop[c] = *reinterpret_cast<const half8 *>(kr + 16 * c);
+            if (c >= kW64QRegs)
+#pragma unroll
+                for (int rb = 0; rb < 2; rb++) qop_l[c & 3][rb] = qop_at(rb, c);
+        }
+#pragma unroll
+        for (int c = 0; c < 16; c++) {
+            if (c + 3 < 16) {
+                kop[(c + 3) & 3] = *reinterpret_cast<const half8 *>(kr + 16 * (c + 3));
+                if (c + 3 >= kW64QRegs)
+#pragma unroll
+                    for (int rb = 0; rb < 2; rb++) qop_l[(c + 3) & 3][rb] = qop_at(rb, c + 3);
+            }
+            const half8 q0 = c < kW64QRegs ? qop[0][c < kW64QRegs ? c : 0] : qop_l[c & 3][0];
+            const half8 q1 = c < kW64QRegs ? qop[1][c < kW64QRegs ? c : 0] : qop_l[c & 3][1];
+            if (c == 0)
+                s_mfma_first(sc[0], kop[c & 3], q0);
+            else
+                s_mfma(sc[0], kop[c & 3], q0);
+            if (c < 8) stage_piece(kdst, vdst, c);          // staging of tile n + 1
+            if (c == 8) stage_scales(vdst, next0);
+            if (c == 0)
+                s_mfma_first(sc[1], kop[c & 3], q1);
+            else if (c < 15)
+                s_mfma(sc[1], kop[c & 3], q1);
+            else
+                s_mfma_last(sc[1], kop[c & 3], q1);
+            if (c == 9) load_raw(next0 + kW64Keys);       // the codes of tile n + 2
+        }
+        load_scales(n, k4, v4);   // for phase B's softmax (staged before the last barrier)
+    };
+
+    // Exponentials of one row block's S (already scaled and shifted by the running maximum, less
+    // `shift`) into P(n) and their sum.
+    auto exp_row = [&](int rb, const floatx16 &s, float shift, const float4 (&v4)[4], half8 (&pn)[2][2])
+        __attribute__((always_inline)) {
+        float lsum = 0.0f;
+#pragma unroll
+        for (int q4 = 0; q4 < 4; q4++) {
+            const float e0 = __builtin_amdgcn_exp2f(s[4 * q4 + 0] - shift);
+            const float e1 = __builtin_amdgcn_exp2f(s[4 * q4 + 1] - shift);
+            const float e2 = __builtin_amdgcn_exp2f(s[4 * q4 + 2] - shift);
+            const float e3 = __builtin_amdgcn_exp2f(s[4 * q4 + 3] - shift);
+            lsum += (e0 + e1) + (e2 + e3);
+            const int u = q4 >> 1, e = 4 * (q4 & 1);
+            pn[rb][u][e + 0] = (_Float16)(e0 * v4[q4].x);   // RNE
+            pn[rb][u][e + 1] = (_Float16)(e1 * v4[q4].y);
+            pn[rb][u][e + 2] = (_Float16)(e2 * v4[q4].z);
+            pn[rb][u][e + 3] = (_Float16)(e3 * v4[q4].w);
+        }
+        return lsum;
+    };
+    auto row_max = [&](const floatx16 &s) __attribute__((always_inline)) {
+        const float ma = max3f(s[0], s[1], s[2]), mb = max3f(s[3], s[4], s[5]), mc = max3f(s[6], s[7], s[8]);
+        const float md = max3f(s[9], s[10], s[11]), me = max3f(s[12], s[13], s[14]);
+        return pair_max(max3f(max3f(ma, mb, mc), max3f(md, me, s[15]), s[15]));
+    };
+
+    // Phase B: O += V(n - 1)^T P(n - 1), interleaved with the common case of the online softmax of
+    // S(n): no causal mask and no row whose maximum grows by more than 2^8, so that P(n) =
+    // exp2(S - m) and l += sum P need no maximum first. The block has no branch (its VALU can fill
+    // the MFMA slots); `need` reports the rows for which the common case does not hold and
+    // fix_softmax below redoes the tile. One code path for every tile (the accumulators must
+    // not meet branches): before the first tile P is zero and the V buffer it reads is
+    // zero-filled; after the last (past), S is -inf, which leaves m, l and P unchanged (zero).
+    auto phase_b = [&](int n, floatx16 (&sc)[2], const float4 (&k4)[4], const float4 (&v4)[4], half8 (&pn)[2][2],
+                       float (&lsum)[2], bool (&need)[2], bool past) __attribute__((always_inline)) {
+        const _Float16 *vt = vbuf[(n + kW64VBufs - 1) % kW64VBufs].v + i * kW64Keys;
+        const int vsw = (i >> 2) & 3;   // rows 32dt + i share the swizzle of row i
+        auto vop = [&](int j) __attribute__((always_inline)) {   // step j: 16-key step u = j / 8, d tile dt = j % 8
+            return *reinterpret_cast<const half8 *>(vt + 32 * (j & 7) * kW64Keys + 8 * ((2 * (j >> 3) + kk) ^ vsw));
+        };
+        half8 va = vop(0), vb = vop(1), vc = vop(2);
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const half8 vn = j + 3 < 16 ? vop(j + 3) : va;
+            o[0][j & 7] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[0][j >> 3], o[0][j & 7], 0, 0, 0);
+            o[1][j & 7] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[1][j >> 3], o[1][j & 7], 0, 0, 0);
+            va = vb;
+            vb = vc;
+            vc = vn;
+        }
+#pragma unroll
+        for (int rb = 0; rb < 2; rb++) {
+            // past the last tile: -inf for every key, whatever the (finite) S and K scales
+            const float add = past ? -INFINITY : -(m[rb] == -INFINITY ? 0.0f : m[rb]);
+#pragma unroll
+            for (int q4 = 0; q4 < 4; q4++) {
+                sc[rb][4 * q4 + 0] = fmaf(sc[rb][4 * q4 + 0], k4[q4].x, add);
+                sc[rb][4 * q4 + 1] = fmaf(sc[rb][4 * q4 + 1], k4[q4].y, add);
+                sc[rb][4 * q4 + 2] = fmaf(sc[rb][4 * q4 + 2], k4[q4].z, add);
+                sc[rb][4 * q4 + 3] = fmaf(sc[rb][4 * q4 + 3], k4[q4].w, add);
+            }
+            const float ymax = row_max(sc[rb]);
+            need[rb] = (ymax > 8.0f) | ((m[rb] == -INFINITY) & (ymax > -INFINITY));   // no branch
+            lsum[rb] = exp_row(rb, sc[rb], 0.0f, v4, pn);
+        }
+#pragma unroll
+        for (int s = 0; s < 16; s++) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // an operand read
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);   // softmax VALU
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+        }
+        // P(n) and l's part are computed here, beside the MFMAs, also where the fix-up below
+        // replaces them (otherwise the compiler moves them into the branch that uses them)
+#pragma unroll
+        for (int rb = 0; rb < 2; rb++) asm volatile("" : "+v"(pn[rb][0]), "+v"(pn[rb][1]), "+v"(lsum[rb]));
+    };
+
+    // The general case of tile n's softmax, after phase B (S scaled and shifted by the running
+    // maximum): the causal mask, the lazy running maximum (a row rebases only when its maximum
+    // grows by more than 2^8, so exponentials stay <= 256) and P(n), l from the rebased S.
+    auto fix_softmax = [&](int n, floatx16 (&sc)[2], const float4 (&v4)[4], half8 (&pn)[2][2], float (&decay)[2],
+                           bool masked) __attribute__((always_inline)) {
+        const uint32_t key0 = kbeg + (uint32_t)n * kW64Keys;
+        if (masked) {
+#pragma unroll
+            for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+                for (int v = 0; v < 16; v++)
+                    if (key0 + 16 * (v >> 3) + 8 * kk + (v & 7) > limit[rb]) sc[rb][v] = -INFINITY;
+        }
+#pragma unroll
+        for (int rb = 0; rb < 2; rb++) {
+            const float ymax = row_max(sc[rb]);
+            const bool rebase = ymax > 8.0f || (m[rb] == -INFINITY && ymax > -INFINITY);
+            const float mref = m[rb] == -INFINITY ? 0.0f : m[rb];
+            const float shift = rebase ? ymax : 0.0f;
+            decay[rb] = rebase ? (m[rb] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(-ymax)) : 1.0f;
+            m[rb] = rebase ? mref + ymax : m[rb];
+            l[rb] = fmaf(l[rb], decay[rb], exp_row(rb, sc[rb], shift, v4, pn));
+        }
+    };
+
+    // In place in the accumulator registers: written as arithmetic, a rescale inside a branch
+    // moves the accumulators out of them. The no-ops cover the wait states between the last MFMA
+    // or VALU write and the accumulator reads and writes.
+    auto rescale = [&](const float (&decay)[2]) __attribute__((always_inline)) {
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
+#pragma unroll
+        for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    float t;
+                    asm volatile(
+                        "v_accvgpr_read_b32 %1, %0\n\ts_nop 1\n\tv_mul_f32 %1, %1, %2\n\ts_nop 1\n\t"
+                        "v_accvgpr_write_b32 %0, %1"
+                        : "+a"(o[rb][dt][e]), "=&v"(t)
+                        : "v"(decay[rb]));
+                }
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
+    };
+
+    for (int n = 0; n <= ntiles; n++) {
+        // the accumulators live in the accumulator registers across iterations
+#pragma unroll
+        for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) asm volatile("" : "+a"(o[rb][dt]));
+        floatx16 sc[2];
+        float4 k4[4], v4[4];
+        if (n < ntiles) {
+            phase_a(n, sc, k4, v4);
+        } else {
+#pragma unroll
+            for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) sc[rb][v] = 0.0f;
+            load_scales(n, k4, v4);   // finite values: staged for keys past the last tile
+        }
+        __syncthreads();
+        half8 pn[2][2];
+        float lsum[2];
+        bool need[2];
+        phase_b(n, sc, k4, v4, pn, lsum, need, n == ntiles);
+        const bool masked = kbeg + (uint32_t)n * kW64Keys + kW64Keys - 1 > wave_min_limit;
+        if (masked | (__ballot(need[0] | need[1]) != 0)) {   // bitwise: both sides computed
+            float decay[2] = {1.0f, 1.0f};
+            fix_softmax(n, sc, v4, pn, decay, masked);
+            // a rebase scales what O holds (through tile n - 1) before P(n) joins it; the first
+            // rebase of a row finds O zero
+            if (__ballot((decay[0] != 1.0f && decay[0] != 0.0f) || (decay[1] != 1.0f && decay[1] != 0.0f)))
+                rescale(decay);
+        } else {
+#pragma unroll
+            for (int rb = 0; rb < 2; rb++) l[rb] += lsum[rb];
+        }
+#pragma unroll
+        for (int rb = 0; rb < 2; rb++) {
+            pb[rb][0] = pn[rb][0];
+            pb[rb][1] = pn[rb][1];
+        }
+    }
+#pragma unroll
+    for (int rb = 0; rb < 2; rb++) l[rb] += __shfl_xor(l[rb], 32, 64);   // the two lanes of a row summed disjoint keys
+
+    // ---- epilogue: lane (i, kk) holds O^T[d][row] for d = 32dt + 8(v/4) + 4kk + v%4
+    if (p.splits == 1) {
+#pragma unroll
+        for (int rb = 0; rb < 2; rb++) {
+            if (!row_valid[rb]) continue;
+            const uint32_t token = my_row[rb] / 8, head = g * 8 + my_row[rb] % 8;
+            const size_t base = ((size_t)token * 16 + head) * 256;
+            const float inv = vs_ref / l[rb];
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+                for (int vq = 0; vq < 4; vq++) {
+                    const int d = 32 * dt + 8 * vq + 4 * kk;
+                    const float4 gv = *reinterpret_cast<const float4 *>(p.gate + base + d);
+                    float4 out;
+                    out.x = o[rb][dt][4 * vq + 0] * inv * sigmoidf(gv.x);
+                    out.y = o[rb][dt][4 * vq + 1] * inv * sigmoidf(gv.y);
+                    out.z = o[rb][dt][4 * vq + 2] * inv * sigmoidf(gv.z);
+                    out.w = o[rb][dt][4 * vq + 3] * inv * sigmoidf(gv.w);
+                    *reinterpret_cast<float4 *>(p.y + base + d) = out;
+                }
+        }
+        return;
+    }
+    // Split partials: O^T / l as FP16 rows through LDS, so that every store instruction writes
+    // 1 KB of whole rows (16-byte pieces of 32 rows each reach HBM as partial lines). Wave w stages
+    // its 64 rows (32 KB, 16-byte chunks XOR-swizzled by row) in a region no other wave uses:
+    // K tiles, V tiles 0-1, V tiles 2-3, the Q^T chunks.
+    static_assert(sizeof(kbuf) >= 32768 && 2 * sizeof(W64VTile) >= 32768 && sizeof(qlds) >= 32768,
+                  "an LDS region per wave holds its 64 FP16 rows");
+    __syncthreads();   // every wave has read its last tile
+    unsigned char *ostage = wave == 0   ? reinterpret_cast<unsigned char *>(kbuf)
+                            : wave == 1 ? reinterpret_cast<unsigned char *>(&vbuf[0])
+                            : wave == 2 ? reinterpret_cast<unsigned char *>(&vbuf[2])
+                                        : reinterpret_cast<unsigned char *>(qlds);
+    unsigned char *pbase = reinterpret_cast<unsigned char *>(p.partial) +
+                           (((size_t)g * p.tiles + tile) * p.splits + split) * kPPPartialBytes;
+    typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int rb = 0; rb < 2; rb++) {
+        const int row = 32 * rb + i;   // of the wave's 64
+        const float inv_l = l[rb] > 0.0f ? 1.0f / l[rb] : 0.0f;
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+            for (int vq = 0; vq < 4; vq++) {
+                const int chunk = 4 * dt + vq;   // dimensions 8 chunk .. 8 chunk + 7; this lane's half at 4 kk
+                const half4 hv = {(_Float16)(o[rb][dt][4 * vq] * inv_l), (_Float16)(o[rb][dt][4 * vq + 1] * inv_l),
+                                  (_Float16)(o[rb][dt][4 * vq + 2] * inv_l), (_Float16)(o[rb][dt][4 * vq + 3] * inv_l)};
+                *reinterpret_cast<half4 *>(ostage + row * 512 + ((chunk ^ (row & 31)) * 16) + 8 * kk) = hv;
+            }
+        if (kk == 0) {
+            const int local_row = 64 * wave + row;
+            float *stat = reinterpret_cast<float *>(pbase + (size_t)kPPRows * 256 * 2);
+            stat[local_row] = m[rb];
+            stat[kPPRows + local_row] = l[rb];
+            stat[2 * kPPRows + local_row] = vs_ref;
+        }
+    }
+    unsigned char *pw = pbase + (size_t)(64 * wave) * 512;   // the wave's rows are contiguous
+#pragma unroll
+    for (int it = 0; it < 32; it++) {
+        const int row = 2 * it + (lane >> 5), chunk = lane & 31;
+        const uint4 v = *reinterpret_cast<const uint4 *>(ostage + row * 512 + ((chunk ^ (row & 31)) * 16));
+        *reinterpret_cast<uint4 *>(pw + (size_t)it * 1024 + lane * 16) = v;
+    }
+}
+
 // Merges the split partials (O^T scaled by vs_ref, m, l in base 2): one wave per
 // logical row, four dimensions per lane, eight splits per step with all their loads
 // in flight together and a running maximum across steps, so a chunk with at most
@@ -848,8 +1337,13 @@ const char *launch_prefill(Context &c, const View *b, const boot_kernel_args &a,
         p.partial = (float *)context_workspace(c, base_blocks * splits * stride_bytes);
         BOOT_REQUIRE(p.partial, "cannot allocate prefill split workspace");
     }
+#ifdef BOOT_PREFILL_PP
     if (int8)
         launch_timed(c, "prefill_pp_kernel", prefill_pp_kernel, dim3((uint32_t)blocks), dim3(512), p);
+#else
+    if (int8)
+        launch_timed(c, "prefill_w64_kernel", prefill_w64_kernel, dim3((uint32_t)blocks), dim3(256), p);
+#endif
     else
         launch_timed(c, "prefill_fp16_kernel", prefill_fp16_kernel, dim3((uint32_t)blocks), dim3(256), p);
     if (splits > 1) {
