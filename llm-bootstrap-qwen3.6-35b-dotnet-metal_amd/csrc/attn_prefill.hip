@@ -327,6 +327,22 @@ __device__ __forceinline__ void s_mfma_last(floatx16 &s, const half8 &a, const h
                  : "+v"(s)
                  : "v"(a), "v"(b));
 }
+// O += A B^T with O in accumulator registers, as assembly for the same reason as s_mfma: the
+// compiler schedules its MFMAs freely and moves operand reads from LDS next to them, exposing
+// their latency. Dependent MFMAs of one chain need no wait states (exact srcC overlap); a vector
+// write of an operand (the FP16 P) precedes these by far more than the two wait states it needs
+// (a work-group barrier and LDS reads lie between); accumulator reads after the chain (rescale,
+// epilogue) are preceded by 24 wait states written beside them.
+__device__ __forceinline__ void o_mfma(floatx16 &o, const half8 &a, const half8 &b) {
+    asm volatile("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(o) : "v"(a), "v"(b));
+}
+// Orders vector work after an assembly MFMA: the registers named here pass through the statement
+// unchanged, so their consumers cannot be scheduled ahead of it (the scheduler places an assembly
+// statement's independent neighbours freely).
+__device__ __forceinline__ void after_mfma(uint32_t &x, uint32_t &y, float &z, float &w) {
+    asm volatile("" : "+v"(x), "+v"(y), "+v"(z), "+v"(w));
+}
+__device__ __forceinline__ void after_mfma(float &z, float &w) { asm volatile("" : "+v"(z), "+v"(w)); }
 
 struct PPTile {
     _Float16 k[kPPKeys * kKStride];        // K codes as FP16, key-major
@@ -702,10 +718,14 @@ __global__ __launch_bounds__(512, 1) void prefill_pp_kernel(PrefillParams p) {
 constexpr int kW64Keys = 32;               // keys per tile
 constexpr int kW64VBufs = 4;               // V^T tiles in LDS
 #ifndef BOOT_W64_QLDS
-#define BOOT_W64_QLDS 5
+#define BOOT_W64_QLDS 7
 #endif
 constexpr int kW64QLds = BOOT_W64_QLDS;    // Q^T chunks per row block kept in LDS, the rest in registers
 constexpr int kW64QRegs = 16 - kW64QLds;
+#ifndef BOOT_W64_VAHEAD
+#define BOOT_W64_VAHEAD 3
+#endif
+constexpr int kW64VAhead = BOOT_W64_VAHEAD;   // V operand reads in flight ahead of the PV MFMAs
 
 struct W64KTile {
     _Float16 k[kW64Keys * kKStride];       // K codes as FP16, key-major (528-byte rows)
@@ -840,9 +860,11 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
     stage(kbuf[0], vbuf[0], kbeg);
     load_raw(kbeg + kW64Keys);
     {
-        // the V^T tile that the PV of "tile -1" reads, with zero probabilities: zero, not NaN
-        uint4 *z = reinterpret_cast<uint4 *>(vbuf[kW64VBufs - 1].v);
-        for (int e = tid; e < 256 * kW64Keys * 2 / 16; e += 256) z[e] = make_uint4(0, 0, 0, 0);
+        // "tile -1", whose zero probabilities the first PV multiplies: zero V^T codes and scales,
+        // not NaN
+        static_assert(sizeof(W64VTile) % 16 == 0, "whole 16-byte stores");
+        uint4 *z = reinterpret_cast<uint4 *>(&vbuf[kW64VBufs - 1]);
+        for (int e = tid; e < (int)(sizeof(W64VTile) / 16); e += 256) z[e] = make_uint4(0, 0, 0, 0);
     }
     __syncthreads();
 
@@ -864,160 +886,189 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
                              : __builtin_bit_cast(half8, qlds[c < kW64QRegs ? 0 : c - kW64QRegs][rb][tid]);
     };
 
-    // the K and V scales of tile n, as the softmax lanes use them
-    auto load_scales = [&](int n, float4 (&k4)[4], float4 (&v4)[4]) __attribute__((always_inline)) {
-        const W64VTile &sb = vbuf[n % kW64VBufs];
+    // the K (or V) scales of tile n's keys (n >= -1), as the softmax lanes hold them
+    auto load_scales = [&](int n, bool v, float4 (&x4)[4]) __attribute__((always_inline)) {
+        const W64VTile &sb = vbuf[(n + kW64VBufs) % kW64VBufs];
+        const float *src = v ? sb.vs : sb.ks;
 #pragma unroll
-        for (int q4 = 0; q4 < 4; q4++) {
-            k4[q4] = *reinterpret_cast<const float4 *>(sb.ks + 16 * (q4 >> 1) + 8 * kk + 4 * (q4 & 1));
-            v4[q4] = *reinterpret_cast<const float4 *>(sb.vs + 16 * (q4 >> 1) + 8 * kk + 4 * (q4 & 1));
-        }
+        for (int q4 = 0; q4 < 4; q4++)
+            x4[q4] = *reinterpret_cast<const float4 *>(src + 16 * (q4 >> 1) + 8 * kk + 4 * (q4 & 1));
     };
 
-    // Phase A of tile n: S(n) for both row blocks, K operands read three steps ahead; the staging
-    // of tile n + 1 and the loads of tile n + 2 are spread between the MFMAs.
-    auto phase_a = [&](int n, floatx16 (&sc)[2], float4 (&k4)[4], float4 (&v4)[4]) __attribute__((always_inline)) {
-        const _Float16 *kr = kbuf[n & 1].k + qk_key_row(i) * kKStride + 8 * kk;
-        const uint32_t next0 = kbeg + (uint32_t)(n + 1) * kW64Keys;
-        W64KTile &kdst = kbuf[(n + 1) & 1];                 // past the last tile: unread buffers
-        W64VTile &vdst = vbuf[(n + 1) % kW64VBufs];
-        half8 kop[4];                                       // K operands, read three steps ahead
-        half8 qop_l[4][2];                                  // Q^T chunks from LDS, likewise
-#pragma unroll
-        for (int c = 0; c < 3; c++) {
-            kop[c] = *reinterpret_cast<const half8 *>(kr + 16 * c);
-            if (c >= kW64QRegs)
-#pragma unroll
-                for (int rb = 0; rb < 2; rb++) qop_l[c & 3][rb] = qop_at(rb, c);
-        }
-#pragma unroll
-        for (int c = 0; c < 16; c++) {
-            if (c + 3 < 16) {
-                kop[(c + 3) & 3] = *reinterpret_cast<const half8 *>(kr + 16 * (c + 3));
-                if (c + 3 >= kW64QRegs)
-#pragma unroll
-                    for (int rb = 0; rb < 2; rb++) qop_l[(c + 3) & 3][rb] = qop_at(rb, c + 3);
-            }
-            const half8 q0 = c < kW64QRegs ? qop[0][c < kW64QRegs ? c : 0] : qop_l[c & 3][0];
-            const half8 q1 = c < kW64QRegs ? qop[1][c < kW64QRegs ? c : 0] : qop_l[c & 3][1];
-            if (c == 0)
-                s_mfma_first(sc[0], kop[c & 3], q0);
-            else
-                s_mfma(sc[0], kop[c & 3], q0);
-            if (c < 8) stage_piece(kdst, vdst, c);          // staging of tile n + 1
-            if (c == 8) stage_scales(vdst, next0);
-            if (c == 0)
-                s_mfma_first(sc[1], kop[c & 3], q1);
-            else if (c < 15)
-                s_mfma(sc[1], kop[c & 3], q1);
-            else
-                s_mfma_last(sc[1], kop[c & 3], q1);
-            if (c == 9) load_raw(next0 + kW64Keys);       // the codes of tile n + 2
-        }
-        load_scales(n, k4, v4);   // for phase B's softmax (staged before the last barrier)
+    // The softmax of tile n - 1, finished in phase A of tile n: element v of row block rb of
+    // exp2(S) with S scaled and shifted by the running maximum, times the key's V scale / vs_ref
+    // into P (FP16, RNE), and into the row's sum.
+    auto exp_elem = [&](int rb, int v, const floatx16 (&sp)[2], const float4 (&v4)[4], half8 (&pn)[2][2],
+                        float (&lsum)[2]) __attribute__((always_inline)) {
+        const float e = __builtin_amdgcn_exp2f(sp[rb][v]);
+        const float4 &w = v4[v >> 2];
+        const float vsc = (v & 3) == 0 ? w.x : (v & 3) == 1 ? w.y : (v & 3) == 2 ? w.z : w.w;
+        pn[rb][v >> 3][v & 7] = (_Float16)(e * vsc);
+        lsum[rb] += e;
     };
 
-    // Exponentials of one row block's S (already scaled and shifted by the running maximum, less
-    // `shift`) into P(n) and their sum.
-    auto exp_row = [&](int rb, const floatx16 &s, float shift, const float4 (&v4)[4], half8 (&pn)[2][2])
+    // Phase A of tile n: S(n) for both row blocks (K operands read three steps ahead), the staging
+    // of tile n + 1, the loads of tile n + 2 and the exponentials of tile n - 1 (P(n - 1) and l),
+    // spread between the MFMAs. One path for every n: after the last tile (n = ntiles) the
+    // MFMAs multiply the finite codes staged for keys past the split, an S that phase B replaces
+    // with -inf, and the staging fills buffers no later phase reads.
+    auto phase_a = [&](int n, floatx16 (&sc)[2], floatx16 (&sp)[2], const float (&dec)[2], half8 (&pn)[2][2])
         __attribute__((always_inline)) {
-        float lsum = 0.0f;
+        float4 v4[4];
+        load_scales(n - 1, true, v4);
+        float lsum[2] = {0.0f, 0.0f};
+        {
+            const _Float16 *kr = kbuf[n & 1].k + qk_key_row(i) * kKStride + 8 * kk;
+            const uint32_t next0 = kbeg + (uint32_t)(n + 1) * kW64Keys;
+            W64KTile &kdst = kbuf[(n + 1) & 1];                 // past the last tile: unread buffers
+            W64VTile &vdst = vbuf[(n + 1) % kW64VBufs];
+            half8 kop[4];                                       // K operands, read three steps ahead
+            half8 qop_l[4][2];                                  // Q^T chunks from LDS, likewise
 #pragma unroll
-        for (int q4 = 0; q4 < 4; q4++) {
-            const float e0 = __builtin_amdgcn_exp2f(s[4 * q4 + 0] - shift);
-            const float e1 = __builtin_amdgcn_exp2f(s[4 * q4 + 1] - shift);
-            const float e2 = __builtin_amdgcn_exp2f(s[4 * q4 + 2] - shift);
-            const float e3 = __builtin_amdgcn_exp2f(s[4 * q4 + 3] - shift);
-            lsum += (e0 + e1) + (e2 + e3);
-            const int u = q4 >> 1, e = 4 * (q4 & 1);
-            pn[rb][u][e + 0] = (_Float16)(e0 * v4[q4].x);   // RNE
-            pn[rb][u][e + 1] = (_Float16)(e1 * v4[q4].y);
-            pn[rb][u][e + 2] = (_Float16)(e2 * v4[q4].z);
-            pn[rb][u][e + 3] = (_Float16)(e3 * v4[q4].w);
+            for (int c = 0; c < 3; c++) {
+                kop[c] = *reinterpret_cast<const half8 *>(kr + 16 * c);
+                if (c >= kW64QRegs)
+#pragma unroll
+                    for (int rb = 0; rb < 2; rb++) qop_l[c & 3][rb] = qop_at(rb, c);
+            }
+#pragma unroll
+            for (int c = 0; c < 16; c++) {
+                if (c + 3 < 16) {
+                    kop[(c + 3) & 3] = *reinterpret_cast<const half8 *>(kr + 16 * (c + 3));
+                    if (c + 3 >= kW64QRegs)
+#pragma unroll
+                        for (int rb = 0; rb < 2; rb++) qop_l[(c + 3) & 3][rb] = qop_at(rb, c + 3);
+                }
+                const half8 q0 = c < kW64QRegs ? qop[0][c < kW64QRegs ? c : 0] : qop_l[c & 3][0];
+                const half8 q1 = c < kW64QRegs ? qop[1][c < kW64QRegs ? c : 0] : qop_l[c & 3][1];
+                // each step's vector work is tied behind its MFMA (after_mfma)
+                if (c == 0)
+                    s_mfma_first(sc[0], kop[c & 3], q0);
+                else
+                    s_mfma(sc[0], kop[c & 3], q0);
+                {
+                    // this step's inputs follow the MFMA, the previous step's row sum precedes it
+                    float z = sp[0][c];
+                    if (c < 8) {
+                        uint4 &r = c < 2 ? rk0 : c < 4 ? rk1 : c < 6 ? rv0 : rv1;
+                        after_mfma((c & 1) ? r.z : r.x, (c & 1) ? r.w : r.y, z, lsum[1]);
+                    } else {
+                        after_mfma(z, lsum[1]);
+                    }
+                    sp[0][c] = z;
+                }
+                if (c < 8) stage_piece(kdst, vdst, c);          // staging of tile n + 1
+                if (c == 8) stage_scales(vdst, next0);
+                exp_elem(0, c, sp, v4, pn, lsum);
+                if (c == 0)
+                    s_mfma_first(sc[1], kop[c & 3], q1);
+                else if (c < 15)
+                    s_mfma(sc[1], kop[c & 3], q1);
+                else
+                    s_mfma_last(sc[1], kop[c & 3], q1);
+                {
+                    float z = sp[1][c];
+                    after_mfma(z, lsum[0]);
+                    sp[1][c] = z;
+                }
+                exp_elem(1, c, sp, v4, pn, lsum);
+                if (c == 9) load_raw(next0 + kW64Keys);       // the codes of tile n + 2
+            }
         }
-        return lsum;
+#pragma unroll
+        for (int rb = 0; rb < 2; rb++) {
+            l[rb] = fmaf(l[rb], dec[rb], lsum[rb]);
+            // P(n - 1) complete here, before the barrier: phase B's assembly MFMAs read it, and
+            // the compiler pads no wait states for them
+            asm volatile("" : "+v"(pn[rb][0]), "+v"(pn[rb][1]));
+        }
     };
+
     auto row_max = [&](const floatx16 &s) __attribute__((always_inline)) {
         const float ma = max3f(s[0], s[1], s[2]), mb = max3f(s[3], s[4], s[5]), mc = max3f(s[6], s[7], s[8]);
         const float md = max3f(s[9], s[10], s[11]), me = max3f(s[12], s[13], s[14]);
         return pair_max(max3f(max3f(ma, mb, mc), max3f(md, me, s[15]), s[15]));
     };
 
-    // Phase B: O += V(n - 1)^T P(n - 1), interleaved with the common case of the online softmax of
-    // S(n): no causal mask and no row whose maximum grows by more than 2^8, so that P(n) =
-    // exp2(S - m) and l += sum P need no maximum first. The block has no branch (its VALU can fill
-    // the MFMA slots); `need` reports the rows for which the common case does not hold and
-    // fix_softmax below redoes the tile. One code path for every tile (the accumulators must
-    // not meet branches): before the first tile P is zero and the V buffer it reads is
-    // zero-filled; after the last (past), S is -inf, which leaves m, l and P unchanged (zero).
-    auto phase_b = [&](int n, floatx16 (&sc)[2], const float4 (&k4)[4], const float4 (&v4)[4], half8 (&pn)[2][2],
-                       float (&lsum)[2], bool (&need)[2], bool past) __attribute__((always_inline)) {
+    // Phase B of tile n: O += V(n - 1)^T P(n - 1) (V operands read kW64VAhead steps ahead),
+    // interleaved with S(n)'s scaling (K scale, log2(e) / 16, less the running maximum) and its row
+    // maxima. `need` reports the rows whose maximum grows by more than 2^8 (or that meet their
+    // first key): fix_softmax handles those and the causal mask. One code path for every tile (the
+    // accumulators must not meet branches): before the first tile P is zero and the V buffer it
+    // reads is zero-filled; after the last (past), S is -inf, which leaves m, l and P unchanged.
+    auto phase_b = [&](int n, floatx16 (&sc)[2], const half8 (&pp)[2][2], bool (&need)[2], float (&ymax)[2], bool past)
+        __attribute__((always_inline)) {
+        float4 k4[4];
+        load_scales(n, false, k4);
+        float add[2];
+#pragma unroll
+        for (int rb = 0; rb < 2; rb++)   // past the last tile: -inf for every key, whatever the (finite) S and K scales
+            add[rb] = past ? -INFINITY : -(m[rb] == -INFINITY ? 0.0f : m[rb]);
         const _Float16 *vt = vbuf[(n + kW64VBufs - 1) % kW64VBufs].v + i * kW64Keys;
         const int vsw = (i >> 2) & 3;   // rows 32dt + i share the swizzle of row i
         auto vop = [&](int j) __attribute__((always_inline)) {   // step j: 16-key step u = j / 8, d tile dt = j % 8
             return *reinterpret_cast<const half8 *>(vt + 32 * (j & 7) * kW64Keys + 8 * ((2 * (j >> 3) + kk) ^ vsw));
         };
-        half8 va = vop(0), vb = vop(1), vc = vop(2);
+        // step j < 8 scales elements 2j, 2j + 1 of each row block; steps 8-9 take the maxima
+        auto scale_pair = [&](int rb, int j) __attribute__((always_inline)) {
+            float x = sc[rb][2 * j], y = sc[rb][2 * j + 1];
+            after_mfma(x, y);
+            const float4 &kq = k4[j >> 1];
+            sc[rb][2 * j] = fmaf(x, (j & 1) ? kq.z : kq.x, add[rb]);
+            sc[rb][2 * j + 1] = fmaf(y, (j & 1) ? kq.w : kq.y, add[rb]);
+        };
+        float mpart[2][2];
+        auto max_piece = [&](int rb, int j) __attribute__((always_inline)) {
+            const floatx16 &t = sc[rb];
+            if (j == 8) {
+                mpart[rb][0] = max3f(max3f(t[0], t[1], t[2]), max3f(t[3], t[4], t[5]), max3f(t[6], t[7], t[8]));
+                mpart[rb][1] = max3f(max3f(t[9], t[10], t[11]), max3f(t[12], t[13], t[14]), t[15]);
+            } else if (j == 9) {
+                ymax[rb] = pair_max(fmaxf(mpart[rb][0], mpart[rb][1]));
+                need[rb] = (ymax[rb] > 8.0f) | ((m[rb] == -INFINITY) & (ymax[rb] > -INFINITY));   // no branch
+            }
+        };
+        half8 vring[kW64VAhead + 1];
+#pragma unroll
+        for (int j = 0; j < kW64VAhead; j++) vring[j] = vop(j);
 #pragma unroll
         for (int j = 0; j < 16; j++) {
-            const half8 vn = j + 3 < 16 ? vop(j + 3) : va;
-            o[0][j & 7] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[0][j >> 3], o[0][j & 7], 0, 0, 0);
-            o[1][j & 7] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[1][j >> 3], o[1][j & 7], 0, 0, 0);
-            va = vb;
-            vb = vc;
-            vc = vn;
+            if (j + kW64VAhead < 16) vring[(j + kW64VAhead) % (kW64VAhead + 1)] = vop(j + kW64VAhead);
+            const half8 va = vring[j % (kW64VAhead + 1)];
+            o_mfma(o[0][j & 7], va, pp[0][j >> 3]);
+            if (j < 8) scale_pair(0, j);
+            else max_piece(0, j);
+            o_mfma(o[1][j & 7], va, pp[1][j >> 3]);
+            if (j < 8) scale_pair(1, j);
+            else max_piece(1, j);
         }
-#pragma unroll
-        for (int rb = 0; rb < 2; rb++) {
-            // past the last tile: -inf for every key, whatever the (finite) S and K scales
-            const float add = past ? -INFINITY : -(m[rb] == -INFINITY ? 0.0f : m[rb]);
-#pragma unroll
-            for (int q4 = 0; q4 < 4; q4++) {
-                sc[rb][4 * q4 + 0] = fmaf(sc[rb][4 * q4 + 0], k4[q4].x, add);
-                sc[rb][4 * q4 + 1] = fmaf(sc[rb][4 * q4 + 1], k4[q4].y, add);
-                sc[rb][4 * q4 + 2] = fmaf(sc[rb][4 * q4 + 2], k4[q4].z, add);
-                sc[rb][4 * q4 + 3] = fmaf(sc[rb][4 * q4 + 3], k4[q4].w, add);
-            }
-            const float ymax = row_max(sc[rb]);
-            need[rb] = (ymax > 8.0f) | ((m[rb] == -INFINITY) & (ymax > -INFINITY));   // no branch
-            lsum[rb] = exp_row(rb, sc[rb], 0.0f, v4, pn);
-        }
-#pragma unroll
-        for (int s = 0; s < 16; s++) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // an operand read
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);   // softmax VALU
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
-        }
-        // P(n) and l's part are computed here, beside the MFMAs, also where the fix-up below
-        // replaces them (otherwise the compiler moves them into the branch that uses them)
-#pragma unroll
-        for (int rb = 0; rb < 2; rb++) asm volatile("" : "+v"(pn[rb][0]), "+v"(pn[rb][1]), "+v"(lsum[rb]));
     };
 
-    // The general case of tile n's softmax, after phase B (S scaled and shifted by the running
-    // maximum): the causal mask, the lazy running maximum (a row rebases only when its maximum
-    // grows by more than 2^8, so exponentials stay <= 256) and P(n), l from the rebased S.
-    auto fix_softmax = [&](int n, floatx16 (&sc)[2], const float4 (&v4)[4], half8 (&pn)[2][2], float (&decay)[2],
-                           bool masked) __attribute__((always_inline)) {
+    // The general case of tile n, after phase B: the causal mask, the lazy running maximum (a row
+    // rebases only when its maximum grows by more than 2^8, so exponentials stay <= 256): S is
+    // shifted by the rebase, `dec` is the factor l takes before tile n's sum joins it.
+    auto fix_softmax = [&](int n, floatx16 (&sc)[2], float (&ymax)[2], float (&dec)[2], bool masked)
+        __attribute__((always_inline)) {
         const uint32_t key0 = kbeg + (uint32_t)n * kW64Keys;
         if (masked) {
 #pragma unroll
-            for (int rb = 0; rb < 2; rb++)
+            for (int rb = 0; rb < 2; rb++) {
 #pragma unroll
                 for (int v = 0; v < 16; v++)
                     if (key0 + 16 * (v >> 3) + 8 * kk + (v & 7) > limit[rb]) sc[rb][v] = -INFINITY;
+                ymax[rb] = row_max(sc[rb]);
+            }
         }
 #pragma unroll
         for (int rb = 0; rb < 2; rb++) {
-            const float ymax = row_max(sc[rb]);
-            const bool rebase = ymax > 8.0f || (m[rb] == -INFINITY && ymax > -INFINITY);
+            const bool rebase = ymax[rb] > 8.0f || (m[rb] == -INFINITY && ymax[rb] > -INFINITY);
             const float mref = m[rb] == -INFINITY ? 0.0f : m[rb];
-            const float shift = rebase ? ymax : 0.0f;
-            decay[rb] = rebase ? (m[rb] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(-ymax)) : 1.0f;
-            m[rb] = rebase ? mref + ymax : m[rb];
-            l[rb] = fmaf(l[rb], decay[rb], exp_row(rb, sc[rb], shift, v4, pn));
+            dec[rb] = rebase ? (m[rb] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(-ymax[rb])) : 1.0f;
+            m[rb] = rebase ? mref + ymax[rb] : m[rb];
+            if (rebase) {
+#pragma unroll
+                for (int v = 0; v < 16; v++) sc[rb][v] = sc[rb][v] - ymax[rb];
+            }
         }
     };
 
@@ -1042,6 +1093,14 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
         asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
     };
 
+    // S(n - 1), scaled and shifted (exp2 of it is P(n - 1) before the V scales), and the factor
+    // l takes before its sum joins: tile -1 has no keys
+    floatx16 sp[2];
+    float dec[2] = {1.0f, 1.0f};
+#pragma unroll
+    for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) sp[rb][v] = -INFINITY;
     for (int n = 0; n <= ntiles; n++) {
         // the accumulators live in the accumulator registers across iterations
 #pragma unroll
@@ -1049,39 +1108,23 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
 #pragma unroll
             for (int dt = 0; dt < 8; dt++) asm volatile("" : "+a"(o[rb][dt]));
         floatx16 sc[2];
-        float4 k4[4], v4[4];
-        if (n < ntiles) {
-            phase_a(n, sc, k4, v4);
-        } else {
-#pragma unroll
-            for (int rb = 0; rb < 2; rb++)
-#pragma unroll
-                for (int v = 0; v < 16; v++) sc[rb][v] = 0.0f;
-            load_scales(n, k4, v4);   // finite values: staged for keys past the last tile
-        }
+        phase_a(n, sc, sp, dec, pb);
         __syncthreads();
-        half8 pn[2][2];
-        float lsum[2];
         bool need[2];
-        phase_b(n, sc, k4, v4, pn, lsum, need, n == ntiles);
+        float ymax[2];
+        phase_b(n, sc, pb, need, ymax, n == ntiles);
+        dec[0] = dec[1] = 1.0f;
         const bool masked = kbeg + (uint32_t)n * kW64Keys + kW64Keys - 1 > wave_min_limit;
         if (masked | (__ballot(need[0] | need[1]) != 0)) {   // bitwise: both sides computed
-            float decay[2] = {1.0f, 1.0f};
-            fix_softmax(n, sc, v4, pn, decay, masked);
+            fix_softmax(n, sc, ymax, dec, masked);
             // a rebase scales what O holds (through tile n - 1) before P(n) joins it; the first
             // rebase of a row finds O zero
-            if (__ballot((decay[0] != 1.0f && decay[0] != 0.0f) || (decay[1] != 1.0f && decay[1] != 0.0f)))
-                rescale(decay);
-        } else {
-#pragma unroll
-            for (int rb = 0; rb < 2; rb++) l[rb] += lsum[rb];
+            if (__ballot((dec[0] != 1.0f && dec[0] != 0.0f) || (dec[1] != 1.0f && dec[1] != 0.0f))) rescale(dec);
         }
 #pragma unroll
-        for (int rb = 0; rb < 2; rb++) {
-            pb[rb][0] = pn[rb][0];
-            pb[rb][1] = pn[rb][1];
-        }
+        for (int rb = 0; rb < 2; rb++) sp[rb] = sc[rb];
     }
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");   // the last MFMAs' results, before O is read
 #pragma unroll
     for (int rb = 0; rb < 2; rb++) l[rb] += __shfl_xor(l[rb], 32, 64);   // the two lanes of a row summed disjoint keys
 
