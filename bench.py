@@ -59,9 +59,8 @@ def upload(device, array):
     return b
 
 
-# the INT8 prefill attention kernel of the library's build: one wave per SIMD (default) or
-# the two-team work-group (built with -DBOOT_PREFILL_PP)
-PREFILL_INT8_KERNELS = ["prefill_w64_kernel", "prefill_pp_kernel"]
+# the INT8 prefill attention kernel (its FP16-KV control: prefill_w64_fp16_kernel)
+PREFILL_INT8_KERNELS = ["prefill_w64_kernel"]
 
 
 def kernel_stats(device, names):
@@ -438,11 +437,12 @@ def main():
     device.reset_wall_timing(kernels_exact=True)
     for _ in range(args.steps):
         control.step()
-    kc = kernel_stats(device, ["prefill_fp16_kernel", "prefill_combine_kernel<128>", "prepare_fused_half_kernel"])
+    kc = kernel_stats(device, ["prefill_w64_fp16_kernel", "prefill_combine_half_kernel", "prepare_fused_half_kernel"])
     result["fp16_kv_control"] = {
         "ms_per_layer": round(fp16_ms, 4),
-        "attention_kernel_ms_per_layer": round(kc["prefill_fp16_kernel"][0] / args.steps, 4),
-        "combine_ms_per_layer": round(kc.get("prefill_combine_kernel<128>", (0.0, 0))[0] / args.steps, 4),
+        "kernel": "prefill_w64_fp16_kernel (the INT8 kernel's schedule with FP16 staging)",
+        "attention_kernel_ms_per_layer": round(kc.get("prefill_w64_fp16_kernel", (0.0, 0))[0] / args.steps, 4),
+        "combine_ms_per_layer": round(kc.get("prefill_combine_half_kernel", (0.0, 0))[0] / args.steps, 4),
         "prepare_ms_per_layer": round(kc["prepare_fused_half_kernel"][0] / args.steps, 4),
         "int8_over_fp16_time": round(wall_ms / fp16_ms, 4),
         "kv_bytes_30k": {"int8_with_scales": 30720 * 1040, "fp16": 30720 * 2048}}

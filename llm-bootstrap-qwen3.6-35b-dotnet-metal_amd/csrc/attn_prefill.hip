@@ -1,5 +1,5 @@
 // Causal online GQA prefill over the INT8 KV cache (block prefill, <= 512-token
-// chunks), MFMA on gfx950.
+// chunks), MFMA on gfx950, and the FP16-KV control on the same schedule.
 //
 // Reference semantics: attention_int8_prefill / attention_online_int8_q32_k256_r2
 // (kernels.metal:1378-1457), dispatched by DeviceAttentionWorkspace.EncodeInt8
@@ -17,10 +17,11 @@
 // BF16 probabilities measure 1.6e-3 to 3.2e-3.
 // Logical row r of KV group g is (token r/8, head 8g + r%8): the grouped FP16
 // query layout of attention_query_grouped_half (kernels.metal:1276-1281).
+// The FP16-KV control (attention_online_q32_k256_s8_g8_r2, kernels.metal:1356-1365:
+// FP16 token-major K and V, no scales) runs the same kernel with FP16 staging, so that
+// the two differ only in the cache they read.
 //
-// gfx950 structure (not the Metal tiling), shared by the INT8 kernel
-// (prefill_pp_kernel) and the FP16-KV control (prefill_fp16_kernel): every wave
-// owns 32 logical rows and computes S^T = K . Q^T and O^T += V^T . P^T with
+// gfx950 structure (not the Metal tiling): S^T = K . Q^T and O^T += V^T . P^T with
 // v_mfma_f32_32x32x16_f16 on FP16 operands staged in LDS (INT8 codes are exact in
 // FP16). Transposed products put one query row per lane column, so row statistics
 // are per-lane and the accumulator rescale needs no cross-lane traffic; the key
@@ -36,14 +37,14 @@
 
 namespace boot {
 
-
 namespace {
 
-constexpr int kRows = 128;                 // logical rows per work-group
-constexpr int kKeys = 64;                  // keys per step
 constexpr int kKStride = 256 + 8;          // FP16 K tile row stride (halves): 528 bytes
-constexpr int kVStride = kKeys + 8;        // FP16 V^T tile row stride (halves): 144 bytes
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kTileRows = 256;             // logical rows per work-group (32 tokens x 8 heads)
+// Split partial of one work-group: O^T / l per row as FP16 (|value| <= 127: a mean of V
+// codes weighted by V scale / vs_ref <= 1), then m, l and vs_ref per row as floats.
+constexpr size_t kPartialBytes = (size_t)kTileRows * 256 * 2 + 3 * kTileRows * 4;
 
 struct PrefillParams {
     const _Float16 *q;      // grouped FP16 [2][M][8][256]
@@ -56,239 +57,16 @@ struct PrefillParams {
     uint32_t rows;          // M tokens in the chunk
     uint32_t pos;           // history
     uint32_t keys;          // K = pos + M
-    uint32_t tiles;         // 128-row tiles per group
+    uint32_t tiles;         // 256-row tiles per group
     uint32_t splits;
-    uint32_t split_keys;    // multiple of kKeys
+    uint32_t split_keys;    // multiple of the 32-key tile
     uint32_t remap;         // 1: XCD-aware block order
 };
-
-constexpr size_t kPartialStride = (size_t)kRows * 256 + 2 * kRows;   // O^T rows + m + l
 
 __device__ inline float sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 // Key row of QK tile row i: bits 2 and 3 of i swapped (see header comment).
 __device__ inline int qk_key_row(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
-
-
-// The FP16 token-major control cache of attention_online_q32_k256_s8_g8_r2
-// (kernels.metal:1356-1365): no scales, FP16 probabilities e (<= 2^8 with the lazy
-// maximum), V transposed into LDS by the staging loop. A work-group of 4 waves owns
-// 128 logical rows (16 tokens x 8 heads) of one KV group and two work-groups share a
-// CU (two waves per SIMD), so that one's MFMA work overlaps the other's softmax.
-__global__ __launch_bounds__(256, 2) void prefill_fp16_kernel(PrefillParams p) {
-    __shared__ __attribute__((aligned(16))) _Float16 klds[kKeys * kKStride];
-    __shared__ __attribute__((aligned(16))) _Float16 vlds[256 * kVStride];
-    __shared__ float kscale[kKeys], vscale[kKeys];
-
-    // ---- block -> (group, tile, split); XCD-aware: blocks sharing a key range
-    // (same group and split) land on the same XCD (round-robin dispatch).
-    uint32_t b = blockIdx.x, g, tile, split;
-    {
-        uint32_t combo;
-        if (p.remap) {
-            const uint32_t xcd = b % 8, idx = b / 8;
-            combo = xcd + 8 * (idx / p.tiles);
-            tile = idx % p.tiles;
-        } else {
-            combo = b / p.tiles;
-            tile = b % p.tiles;
-        }
-        g = combo % 2;
-        split = combo / 2;
-    }
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int i = lane & 31, kk = lane >> 5;
-    const uint32_t R = p.rows * 8;
-    const uint32_t r0 = tile * kRows;
-    const uint32_t my_row = r0 + 32 * wave + i;
-    const bool row_valid = my_row < R;
-    const uint32_t rr = row_valid ? my_row : R - 1;
-    const uint32_t limit = p.pos + rr / 8;                              // keys <= limit visible
-    const uint32_t tile_last = min(R - 1, r0 + kRows - 1);
-    const uint32_t tile_end = p.pos + tile_last / 8 + 1;               // keys [0, tile_end)
-    const uint32_t kbeg = split * p.split_keys;
-    const uint32_t kend = min(tile_end, kbeg + p.split_keys);
-    const uint32_t wave_first = min(R - 1, r0 + 32 * wave);
-    const uint32_t wave_min_limit = p.pos + wave_first / 8;
-
-    // ---- Q^T operands (B of the QK product): lane (i, kk), dims 16c + 8kk + [0, 8)
-    half8 qop[16];
-    {
-        const _Float16 *qrow = p.q + ((size_t)g * R + rr) * 256 + 8 * kk;
-#pragma unroll
-        for (int c = 0; c < 16; c++) qop[c] = *reinterpret_cast<const half8 *>(qrow + 16 * c);
-    }
-
-    const int tid = threadIdx.x;
-
-    floatx16 o[8];
-#pragma unroll
-    for (int dt = 0; dt < 8; dt++)
-#pragma unroll
-        for (int v = 0; v < 16; v++) o[dt][v] = 0.0f;
-    float m = -INFINITY, l = 0.0f;
-
-    for (uint32_t key0 = kbeg; key0 < kend; key0 += kKeys) {
-        __syncthreads();   // previous tile fully consumed
-        // ---- stage 64 keys: K rows copied as they are, V rows transposed into V^T;
-        // thread: key key0 + tid/4, 64 values
-        {
-            const int krow = tid >> 2, part = tid & 3;
-            const uint32_t key = min(key0 + krow, p.keys - 1);
-            const uint4 *ksrc = reinterpret_cast<const uint4 *>((const _Float16 *)p.k + ((size_t)key * 2 + g) * 256 + part * 64);
-            uint4 *kdst = reinterpret_cast<uint4 *>(klds + krow * kKStride);
-            const _Float16 *vsrc = (const _Float16 *)p.v + ((size_t)key * 2 + g) * 256 + part * 64;
-#pragma unroll
-            for (int j = 0; j < 8; j++) kdst[part * 8 + j] = ksrc[j];
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const uint4 w = *reinterpret_cast<const uint4 *>(vsrc + 8 * j);
-                const _Float16 *hv = reinterpret_cast<const _Float16 *>(&w);
-#pragma unroll
-                for (int e = 0; e < 8; e++) vlds[(part * 64 + 8 * j + e) * kVStride + krow] = hv[e];
-            }
-        }
-        if (tid < kKeys) {
-            const bool inside = key0 + tid < p.keys;   // poisoned tails beyond K never reach P
-            kscale[tid] = kLog2e / 16.0f;
-            vscale[tid] = inside ? 1.0f : 0.0f;
-        }
-        __syncthreads();
-
-        // ---- S^T = K . Q^T, two 32-key tiles
-        floatx16 s[2];
-#pragma unroll
-        for (int a = 0; a < 2; a++) {
-            floatx16 acc;
-#pragma unroll
-            for (int v = 0; v < 16; v++) acc[v] = 0.0f;
-            const int kr = 32 * a + qk_key_row(i);
-            const half8 *krow = reinterpret_cast<const half8 *>(klds + kr * kKStride);
-#pragma unroll
-            for (int c = 0; c < 16; c++)
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(krow[2 * c + kk], qop[c], acc, 0, 0, 0);
-            s[a] = acc;
-        }
-
-        // ---- online softmax for this lane's row; lane value v of tile a is key
-        // key0 + 32a + 16(v/8) + 8kk + v%8.
-        const bool masking = key0 + kKeys - 1 > wave_min_limit;
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int a = 0; a < 2; a++)
-#pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int local = 32 * a + 16 * (v >> 3) + 8 * kk + (v & 7);
-                float x = s[a][v] * kscale[local];
-                if (masking && key0 + local > limit) x = -INFINITY;
-                s[a][v] = x;
-                tmax = fmaxf(tmax, x);
-            }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        // lazy running maximum: rebase (and rescale the accumulator) only when a
-        // row's maximum grows by more than 2^8; exponentials stay <= 256
-        const bool rebase = tmax > m + 8.0f || (m == -INFINITY && tmax > -INFINITY);
-        const float mnew = rebase ? tmax : m;
-        const float mref = mnew == -INFINITY ? 0.0f : mnew;
-        const float decay = rebase ? (m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mnew)) : 1.0f;
-        float rowsum = 0.0f;
-        uint32_t pw[2][8];
-#pragma unroll
-        for (int a = 0; a < 2; a++)
-#pragma unroll
-            for (int v = 0; v < 16; v += 2) {
-                const int local = 32 * a + 16 * (v >> 3) + 8 * kk + (v & 7);
-                const float e0 = __builtin_amdgcn_exp2f(s[a][v] - mref);
-                const float e1 = __builtin_amdgcn_exp2f(s[a][v + 1] - mref);
-                rowsum += e0 + e1;
-                const half2v ph = {(_Float16)(e0 * vscale[local]), (_Float16)(e1 * vscale[local + 1])};   // RNE
-                pw[a][v / 2] = __builtin_bit_cast(uint32_t, ph);
-            }
-        rowsum += __shfl_xor(rowsum, 32, 64);
-        l = l * decay + rowsum;
-        m = mnew;
-        if (__ballot(decay != 1.0f)) {
-#pragma unroll
-            for (int dt = 0; dt < 8; dt++) o[dt] *= decay;
-        }
-
-        // ---- O^T += V^T . P^T; PV step u takes keys 16u + 8kk + [0, 8) = tile u/2, values 8(u%2)..
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const half8 pb = __builtin_bit_cast(
-                half8, make_uint4(pw[u >> 1][4 * (u & 1)], pw[u >> 1][4 * (u & 1) + 1], pw[u >> 1][4 * (u & 1) + 2],
-                                  pw[u >> 1][4 * (u & 1) + 3]));
-            const _Float16 *vrow = vlds + i * kVStride + 16 * u + 8 * kk;
-#pragma unroll
-            for (int dt = 0; dt < 8; dt++)
-                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                    *reinterpret_cast<const half8 *>(vrow + 32 * dt * kVStride), pb, o[dt], 0, 0, 0);
-        }
-    }
-
-    // ---- epilogue: lane (i, kk) holds O^T[d][row] for d = 32dt + 8(v/4) + 4kk + v%4
-    if (p.splits == 1) {
-        if (!row_valid) return;
-        const uint32_t token = my_row / 8, head = g * 8 + my_row % 8;
-        const size_t base = ((size_t)token * 16 + head) * 256;
-        const float inv = 1.0f / l;
-#pragma unroll
-        for (int dt = 0; dt < 8; dt++)
-#pragma unroll
-            for (int vq = 0; vq < 4; vq++) {
-                const int d = 32 * dt + 8 * vq + 4 * kk;
-                const float4 gv = *reinterpret_cast<const float4 *>(p.gate + base + d);
-                float4 out;
-                out.x = o[dt][4 * vq + 0] * inv * sigmoidf(gv.x);
-                out.y = o[dt][4 * vq + 1] * inv * sigmoidf(gv.y);
-                out.z = o[dt][4 * vq + 2] * inv * sigmoidf(gv.z);
-                out.w = o[dt][4 * vq + 3] * inv * sigmoidf(gv.w);
-                *reinterpret_cast<float4 *>(p.y + base + d) = out;
-            }
-        return;
-    }
-    float *part = p.partial + (((size_t)g * p.tiles + tile) * p.splits + split) * kPartialStride;
-    const int local_row = 32 * wave + i;
-#pragma unroll
-    for (int dt = 0; dt < 8; dt++)
-#pragma unroll
-        for (int vq = 0; vq < 4; vq++) {
-            const int d = 32 * dt + 8 * vq + 4 * kk;
-            *reinterpret_cast<float4 *>(part + (size_t)local_row * 256 + d) =
-                make_float4(o[dt][4 * vq], o[dt][4 * vq + 1], o[dt][4 * vq + 2], o[dt][4 * vq + 3]);
-        }
-    if (kk == 0) {
-        part[(size_t)kRows * 256 + local_row] = m;
-        part[(size_t)kRows * 256 + kRows + local_row] = l;
-    }
-}
-
-// ---------------------------------------------------------------- INT8 prefill, two-team schedule
-//
-// A work-group of 8 waves owns 256 logical rows (32 tokens x 8 heads) of one KV
-// group and walks its key range in 32-key tiles. Waves w and w + 4 share a SIMD;
-// waves 0-3 form team 0, waves 4-7 team 1. The loop runs in slots separated by
-// work-group barriers, and in every slot one team issues its MFMAs (O^T += V^T P^T
-// for the previous tile, then S^T = K Q^T for the current one) while the other
-// team runs the VALU work (online softmax of its S and half of the INT8 -> FP16
-// staging of the next tile: team 0 converts K, team 1 the V page slice). The
-// MFMA pipe of each SIMD thus alternates between its two waves while the other
-// wave's VALU instructions issue beside it, instead of both waves waiting on the
-// same barrier with the same kind of work. Tiles live in two LDS buffers; the raw
-// codes of the tile after next are loaded into registers a full iteration ahead.
-//
-// Schedule (n = tile): slot 2n: team 0 MFMA(n), team 1 VALU(n-1);
-//                      slot 2n+1: team 0 VALU(n), team 1 MFMA(n).
-// VALU(n) of team 0 writes K, scales of tile n+1 into buffer (n+1)&1, whose tile
-// n-1 was last read in slot 2n-1; VALU(n) of team 1 (slot 2n+2) writes V of tile
-// n+1, whose buffer was last read in slot 2n+1.
-constexpr int kPPRows = 256;               // logical rows per work-group
-constexpr int kPPKeys = 32;                // keys per tile
-constexpr int kPPVStride = kPPKeys + 8;    // FP16 V^T tile row stride (halves): 80 bytes
-// Split partial of one work-group: O^T / l per row as FP16 (|value| <= 127: a mean of V
-// codes weighted by V scale / vs_ref <= 1), then m, l and vs_ref per row as floats.
-constexpr size_t kPPPartialBytes = (size_t)kPPRows * 256 * 2 + 3 * kPPRows * 4;
-constexpr int kPPQRegs = 6;                // Q^T operand chunks held in registers; the rest in LDS
 
 // Max over the lane pair (l, l ^ 32). v_permlane32_swap exchanges lanes 32-63 of
 // its first operand with lanes 0-31 of its second, so with both holding x every
@@ -339,382 +117,32 @@ __device__ __forceinline__ void o_mfma(floatx16 &o, const half8 &a, const half8 
 // Orders vector work after an assembly MFMA: the registers named here pass through the statement
 // unchanged, so their consumers cannot be scheduled ahead of it (the scheduler places an assembly
 // statement's independent neighbours freely).
-__device__ __forceinline__ void after_mfma(uint32_t &x, uint32_t &y, float &z, float &w) {
+__device__ __forceinline__ void after_mfma(float &z, float &w) { asm volatile("" : "+v"(z), "+v"(w)); }
+__device__ __forceinline__ void after_mfma(uint32_t &x, uint32_t &y) { asm volatile("" : "+v"(x), "+v"(y)); }
+__device__ __forceinline__ void after_mfma(uint32_t &x, uint32_t &y, uint32_t &z, uint32_t &w) {
     asm volatile("" : "+v"(x), "+v"(y), "+v"(z), "+v"(w));
 }
-__device__ __forceinline__ void after_mfma(float &z, float &w) { asm volatile("" : "+v"(z), "+v"(w)); }
 
-struct PPTile {
-    _Float16 k[kPPKeys * kKStride];        // K codes as FP16, key-major
-    _Float16 v[256 * kPPVStride];          // V^T codes as FP16, dimension-major
-    float ks[kPPKeys];                     // K scale * log2(e) / 16
-    float vs[kPPKeys];                     // V scale / vs_ref
-};
-
-__global__ __launch_bounds__(512, 1) void prefill_pp_kernel(PrefillParams p) {
-    __shared__ PPTile buf[2];
-    __shared__ uint4 qlds[16 - kPPQRegs][512];   // each lane's own Q^T operands for chunks kPPQRegs..15
-    __shared__ float vs_partial[8];
-
-    uint32_t g, tile, split;
-    {
-        const uint32_t b = blockIdx.x;
-        uint32_t combo;
-        if (p.remap) {
-            const uint32_t xcd = b % 8, idx = b / 8;
-            combo = xcd + 8 * (idx / p.tiles);
-            tile = idx % p.tiles;
-        } else {
-            combo = b / p.tiles;
-            tile = b % p.tiles;
-        }
-        g = combo % 2;
-        split = combo / 2;
-    }
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int team = wave >> 2;
-    const int t = tid & 255;
-    const int i = lane & 31, kk = lane >> 5;
-    const uint32_t R = p.rows * 8;
-    const uint32_t r0 = tile * kPPRows;
-    const uint32_t my_row = r0 + 32 * wave + i;
-    const bool row_valid = my_row < R;
-    const uint32_t rr = row_valid ? my_row : R - 1;
-    const uint32_t limit = p.pos + rr / 8;                              // keys <= limit visible
-    const uint32_t tile_last = min(R - 1, r0 + kPPRows - 1);
-    const uint32_t tile_end = p.pos + tile_last / 8 + 1;               // keys [0, tile_end)
-    const uint32_t kbeg = split * p.split_keys;
-    const uint32_t kend = min(tile_end, kbeg + p.split_keys);
-    const int ntiles = kend > kbeg ? (int)((kend - kbeg + kPPKeys - 1) / kPPKeys) : 0;
-    const uint32_t wave_min_limit = p.pos + min(R - 1, r0 + 32 * wave) / 8;
-
-    float vs_ref = 0.0f, vs_inv = 0.0f;   // set once the prologue's loads are in (below)
-    // Staging of the FP16 tiles. Team 0 thread t (wave t / 64 of the team, lane t % 64): K rows
-    // 8 (t / 64) + 4j + (t % 64) / 16 for j = 0, 1, 16 codes at 16 (t % 16); a load
-    // instruction reads four whole 256-byte rows. Team 1 thread t: dimension t of
-    // the V^T tile, the 32 codes of its page row. Team 0 threads t < 32 also carry
-    // the K and V scales of key t (loaded one tile ahead of their store).
-    const int8_t *kcodes = (const int8_t *)p.k;
-    const int8_t *vcodes = (const int8_t *)p.v;
-    uint4 raw0 = make_uint4(0, 0, 0, 0), raw1 = raw0;
-    float pre_ks = 0.0f, pre_vs = 0.0f;
-    const int krow0 = 8 * (t >> 6) + ((t & 63) >> 4), kchunk = t & 15;
-    auto load_raw = [&](uint32_t key0) {
-        if (team == 0) {
-            const uint32_t ka = min(key0 + (uint32_t)krow0, p.keys - 1);
-            const uint32_t kb2 = min(key0 + (uint32_t)krow0 + 4, p.keys - 1);
-            const uint32_t offa = (ka * 2 + g) * 256 + kchunk * 16, offb = (kb2 * 2 + g) * 256 + kchunk * 16;   // < 2^27
-            raw0 = *reinterpret_cast<const uint4 *>(kcodes + (size_t)offa);
-            raw1 = *reinterpret_cast<const uint4 *>(kcodes + (size_t)offb);
-        } else {
-            const uint32_t off = (uint32_t)value_index((uint64_t)key0 * 2 + g, 0) + (uint32_t)t * 256;
-            const uint4 *src = reinterpret_cast<const uint4 *>(vcodes + off);
-            raw0 = src[0];
-            raw1 = src[1];
-        }
-    };
-    auto load_scales = [&](uint32_t key0) {
-        if (team == 0 && t < kPPKeys) {
-            // raw scales; they are scaled when stored, a full iteration later, so the
-            // wave never waits for these loads here
-            const size_t at = (size_t)min(key0 + t, p.keys - 1) * 2 + g;
-            pre_ks = p.ks[at];
-            pre_vs = p.vs[at];
-        }
-    };
-    auto store_scales = [&](PPTile &b, uint32_t key0) {
-        if (team == 0 && t < kPPKeys) {
-            const bool inside = key0 + t < p.keys;   // poisoned tails beyond K never reach S or P
-            b.ks[t] = inside ? pre_ks * (kLog2e / 16.0f) : 0.0f;
-            b.vs[t] = inside ? pre_vs * vs_inv : 0.0f;
-        }
-    };
-    // quad q (0..3) of the thread's converted codes: dwords 2q, 2q + 1 of raw0, raw1
-    auto quad_dst = [&](PPTile &b, int q) {
-        return team == 0 ? reinterpret_cast<uint4 *>(b.k + (krow0 + 4 * (q >> 1)) * kKStride + kchunk * 16 + 8 * (q & 1))
-                         : reinterpret_cast<uint4 *>(b.v + t * kPPVStride + 8 * q);
-    };
-    auto convert_quad = [&](int q) {
-        const uint32_t w0 = q == 0 ? raw0.x : q == 1 ? raw0.z : q == 2 ? raw1.x : raw1.z;
-        const uint32_t w1 = q == 0 ? raw0.y : q == 1 ? raw0.w : q == 2 ? raw1.y : raw1.w;
-        uint4 h;
-        i8x4_to_f16(w0, h.x, h.y);
-        i8x4_to_f16(w1, h.z, h.w);
-        return h;
-    };
-
-    // The prologue's loads go out together (one memory round trip): the V scales of
-    // the block's first 4096 keys (vs_ref), the codes and scales of tile 0, the query.
-    float vsv[8];
-#pragma unroll
-    for (int it = 0; it < 8; it++) {
-        const uint32_t key = kbeg + tid + 512 * it;
-        vsv[it] = key < kend ? p.vs[(size_t)key * 2 + g] : 0.0f;
-    }
-    if (ntiles > 0) {
-        load_raw(kbeg);
-        load_scales(kbeg);
-    }
-    // Q^T operands (B of the QK product): lane (i, kk), dims 16c + 8kk + [0, 8); the
-    // last chunks wait in LDS, each lane reading back only what it wrote
-    half8 qop[kPPQRegs];
-    {
-        const _Float16 *qrow = p.q + ((size_t)g * R + rr) * 256 + 8 * kk;
-#pragma unroll
-        for (int c = 0; c < kPPQRegs; c++) qop[c] = *reinterpret_cast<const half8 *>(qrow + 16 * c);
-#pragma unroll
-        for (int c = kPPQRegs; c < 16; c++) qlds[c - kPPQRegs][tid] = *reinterpret_cast<const uint4 *>(qrow + 16 * c);
-    }
-
-    // vs_ref: the largest V scale over this block's keys (0 if all are 0)
-#pragma unroll
-    for (int it = 0; it < 8; it++) vs_ref = fmaxf(vs_ref, vsv[it]);
-    for (uint32_t key = kbeg + tid + 4096; key < kend; key += 512) vs_ref = fmaxf(vs_ref, p.vs[(size_t)key * 2 + g]);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) vs_ref = fmaxf(vs_ref, __shfl_xor(vs_ref, o, 64));
-    if (lane == 0) vs_partial[wave] = vs_ref;
-    __syncthreads();
-    vs_ref = vs_partial[0];
-#pragma unroll
-    for (int w = 1; w < 8; w++) vs_ref = fmaxf(vs_ref, vs_partial[w]);
-    // work-group uniform: scalar registers
-    vs_ref = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, vs_ref)));
-    vs_inv = __builtin_bit_cast(
-        float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, vs_ref > 0.0f ? 1.0f / vs_ref : 0.0f)));
-
-    if (ntiles > 0) {
-#pragma unroll
-        for (int q = 0; q < 4; q++) *quad_dst(buf[0], q) = convert_quad(q);
-        store_scales(buf[0], kbeg);
-        if (ntiles > 1) {
-            load_raw(kbeg + kPPKeys);
-            load_scales(kbeg + kPPKeys);
-        }
-    }
-    __syncthreads();
-
-    floatx16 o[8];
-#pragma unroll
-    for (int dt = 0; dt < 8; dt++)
-#pragma unroll
-        for (int v = 0; v < 16; v++) o[dt][v] = 0.0f;
-    float m = -INFINITY, l = 0.0f;
-    floatx16 s;
-#pragma unroll
-    for (int v = 0; v < 16; v++) s[v] = 0.0f;
-    half8 pb[2];
-#pragma unroll
-    for (int e = 0; e < 8; e++) pb[0][e] = pb[1][e] = (_Float16)0.0f;
-
-    const int slots = 2 * ntiles + 2;
-    for (int slot = 0; slot < slots; slot++) {
-        const int phase = slot - team;
-        if (phase >= 0) {
-            const int n = phase >> 1;
-            if ((phase & 1) == 0) {
-                // ---- MFMA work: O^T += V^T(n-1) . P^T(n-1) and S^T = K(n) . Q^T. The two
-                // products are interleaved (the QK accumulation chain always has an
-                // independent PV product between its steps) and every operand is read
-                // from LDS two steps before its MFMA.
-                const _Float16 *vt = buf[(n - 1) & 1].v + i * kPPVStride + 8 * kk;
-                const _Float16 *kr = buf[n & 1].k + qk_key_row(i) * kKStride + 8 * kk;
-                auto vop = [&](int j) {   // PV step j: u = j / 8, dt = j % 8
-                    return *reinterpret_cast<const half8 *>(vt + 32 * (j & 7) * kPPVStride + 16 * (j >> 3));
-                };
-                auto kop = [&](int c) { return *reinterpret_cast<const half8 *>(kr + 16 * c); };
-                auto qop_at = [&](int c) {
-                    return c < kPPQRegs ? qop[c < kPPQRegs ? c : 0]
-                                        : __builtin_bit_cast(half8, qlds[c < kPPQRegs ? 0 : c - kPPQRegs][tid]);
-                };
-                if (n >= 1 && n < ntiles) {
-#pragma unroll
-                    for (int v = 0; v < 16; v++) s[v] = 0.0f;
-                    half8 va = vop(0), ka = kop(0), qa = qop_at(0);
-                    half8 vb = vop(1), kb = kop(1), qb = qop_at(1);
-#pragma unroll
-                    for (int j = 0; j < 16; j++) {
-                        half8 vc = va, kc = ka, qc = qa;
-                        if (j + 2 < 16) {
-                            vc = vop(j + 2);
-                            kc = kop(j + 2);
-                            qc = qop_at(j + 2);
-                        }
-                        // keep the reads of step j + 2 ahead of the MFMAs of step j
-                        __builtin_amdgcn_sched_barrier(0);
-                        o[j & 7] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[j >> 3], o[j & 7], 0, 0, 0);
-                        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qa, s, 0, 0, 0);
-                        __builtin_amdgcn_sched_barrier(0);
-                        va = vb; ka = kb; qa = qb;
-                        vb = vc; kb = kc; qb = qc;
-                    }
-                } else if (n >= 1) {
-                    half8 va = vop(0), vb = vop(1);
-#pragma unroll
-                    for (int j = 0; j < 16; j++) {
-                        half8 vc = va;
-                        if (j + 2 < 16) vc = vop(j + 2);
-                        __builtin_amdgcn_sched_barrier(0);
-                        o[j & 7] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[j >> 3], o[j & 7], 0, 0, 0);
-                        __builtin_amdgcn_sched_barrier(0);
-                        va = vb;
-                        vb = vc;
-                    }
-                } else if (n < ntiles) {
-#pragma unroll
-                    for (int v = 0; v < 16; v++) s[v] = 0.0f;
-                    half8 ka = kop(0), qa = qop_at(0), kb = kop(1), qb = qop_at(1);
-#pragma unroll
-                    for (int c = 0; c < 16; c++) {
-                        half8 kc = ka, qc = qa;
-                        if (c + 2 < 16) {
-                            kc = kop(c + 2);
-                            qc = qop_at(c + 2);
-                        }
-                        __builtin_amdgcn_sched_barrier(0);
-                        s = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qa, s, 0, 0, 0);
-                        __builtin_amdgcn_sched_barrier(0);
-                        ka = kb; qa = qb;
-                        kb = kc; qb = qc;
-                    }
-                }
-            } else if (n < ntiles) {
-                // ---- VALU work: the online softmax of tile n (lane value v is key
-                // key0 + 16(v/8) + 8kk + v%8), then the staging of tile n+1 and the
-                // prefetch of tile n+2. Staged last, the LDS writes (queued behind the
-                // other team's operand reads) complete while this wave waits at the
-                // barrier instead of delaying the softmax's scale reads.
-                const uint32_t key0 = kbeg + (uint32_t)n * kPPKeys;
-                const PPTile &b = buf[n & 1];
-                float4 k4[4];
-#pragma unroll
-                for (int q4 = 0; q4 < 4; q4++)
-                    k4[q4] = *reinterpret_cast<const float4 *>(b.ks + 16 * (q4 >> 1) + 8 * kk + 4 * (q4 & 1));
-                const float mref = m == -INFINITY ? 0.0f : m;
-#pragma unroll
-                for (int q4 = 0; q4 < 4; q4++) {
-                    s[4 * q4 + 0] = fmaf(s[4 * q4 + 0], k4[q4].x, -mref);
-                    s[4 * q4 + 1] = fmaf(s[4 * q4 + 1], k4[q4].y, -mref);
-                    s[4 * q4 + 2] = fmaf(s[4 * q4 + 2], k4[q4].z, -mref);
-                    s[4 * q4 + 3] = fmaf(s[4 * q4 + 3], k4[q4].w, -mref);
-                }
-                if (key0 + kPPKeys - 1 > wave_min_limit) {
-#pragma unroll
-                    for (int v = 0; v < 16; v++)
-                        if (key0 + 16 * (v >> 3) + 8 * kk + (v & 7) > limit) s[v] = -INFINITY;
-                }
-                const float ma = max3f(s[0], s[1], s[2]), mb = max3f(s[3], s[4], s[5]), mc = max3f(s[6], s[7], s[8]);
-                const float md = max3f(s[9], s[10], s[11]), me = max3f(s[12], s[13], s[14]);
-                const float ymax = pair_max(max3f(max3f(ma, mb, mc), max3f(md, me, s[15]), s[15]));
-                // lazy running maximum: rebase (and rescale the accumulator) only when a
-                // row's maximum grows by more than 2^8; exponentials stay <= 256
-                const bool rebase = ymax > 8.0f || (m == -INFINITY && ymax > -INFINITY);
-                if (__ballot(rebase)) {
-                    float decay = 1.0f, shift = 0.0f;
-                    if (rebase) {
-                        shift = ymax;
-                        decay = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(-ymax);
-                        m = mref + ymax;
-                    }
-#pragma unroll
-                    for (int v = 0; v < 16; v++) s[v] -= shift;
-                    l *= decay;
-#pragma unroll
-                    for (int dt = 0; dt < 8; dt++) o[dt] *= decay;
-                }
-                float lsum = 0.0f;
-#pragma unroll
-                for (int q4 = 0; q4 < 4; q4++) {
-                    const float4 v4 = *reinterpret_cast<const float4 *>(b.vs + 16 * (q4 >> 1) + 8 * kk + 4 * (q4 & 1));
-                    const float e0 = __builtin_amdgcn_exp2f(s[4 * q4 + 0]);
-                    const float e1 = __builtin_amdgcn_exp2f(s[4 * q4 + 1]);
-                    const float e2 = __builtin_amdgcn_exp2f(s[4 * q4 + 2]);
-                    const float e3 = __builtin_amdgcn_exp2f(s[4 * q4 + 3]);
-                    lsum += (e0 + e1) + (e2 + e3);
-                    const int u = q4 >> 1, e = 4 * (q4 & 1);
-                    pb[u][e + 0] = (_Float16)(e0 * v4.x);        // RNE
-                    pb[u][e + 1] = (_Float16)(e1 * v4.y);
-                    pb[u][e + 2] = (_Float16)(e2 * v4.z);
-                    pb[u][e + 3] = (_Float16)(e3 * v4.w);
-                }
-                l += lsum;
-                if (n + 1 < ntiles) {
-                    // tile n+1: team 0 writes K and the scales (buffer last read in slot
-                    // 2n - 1, scales in slot 2n), team 1 writes V (last read in slot 2n + 1)
-                    PPTile &nb = buf[(n + 1) & 1];
-#pragma unroll
-                    for (int q = 0; q < 4; q++) *quad_dst(nb, q) = convert_quad(q);
-                    store_scales(nb, key0 + kPPKeys);
-                    if (n + 2 < ntiles) {
-                        load_raw(key0 + 2 * kPPKeys);
-                        load_scales(key0 + 2 * kPPKeys);
-                    }
-                }
-            }
-        }
-        __syncthreads();
-    }
-    l += __shfl_xor(l, 32, 64);   // the two lanes of a row summed disjoint keys
-
-    // ---- epilogue: lane (i, kk) holds O^T[d][row] for d = 32dt + 8(v/4) + 4kk + v%4
-    if (p.splits == 1) {
-        if (!row_valid) return;
-        const uint32_t token = my_row / 8, head = g * 8 + my_row % 8;
-        const size_t base = ((size_t)token * 16 + head) * 256;
-        const float inv = vs_ref / l;
-#pragma unroll
-        for (int dt = 0; dt < 8; dt++)
-#pragma unroll
-            for (int vq = 0; vq < 4; vq++) {
-                const int d = 32 * dt + 8 * vq + 4 * kk;
-                const float4 gv = *reinterpret_cast<const float4 *>(p.gate + base + d);
-                float4 out;
-                out.x = o[dt][4 * vq + 0] * inv * sigmoidf(gv.x);
-                out.y = o[dt][4 * vq + 1] * inv * sigmoidf(gv.y);
-                out.z = o[dt][4 * vq + 2] * inv * sigmoidf(gv.z);
-                out.w = o[dt][4 * vq + 3] * inv * sigmoidf(gv.w);
-                *reinterpret_cast<float4 *>(p.y + base + d) = out;
-            }
-        return;
-    }
-    unsigned char *pbase = reinterpret_cast<unsigned char *>(p.partial) +
-                           (((size_t)g * p.tiles + tile) * p.splits + split) * kPPPartialBytes;
-    const int local_row = 32 * wave + i;
-    const float inv_l = l > 0.0f ? 1.0f / l : 0.0f;
-    typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-    _Float16 *po = reinterpret_cast<_Float16 *>(pbase) + (size_t)local_row * 256;
-#pragma unroll
-    for (int dt = 0; dt < 8; dt++)
-#pragma unroll
-        for (int vq = 0; vq < 4; vq++) {
-            const int d = 32 * dt + 8 * vq + 4 * kk;
-            const half4 hv = {(_Float16)(o[dt][4 * vq] * inv_l), (_Float16)(o[dt][4 * vq + 1] * inv_l),
-                              (_Float16)(o[dt][4 * vq + 2] * inv_l), (_Float16)(o[dt][4 * vq + 3] * inv_l)};
-            *reinterpret_cast<half4 *>(po + d) = hv;
-        }
-    if (kk == 0) {
-        float *stat = reinterpret_cast<float *>(pbase + (size_t)kPPRows * 256 * 2);
-        stat[local_row] = m;
-        stat[kPPRows + local_row] = l;
-        stat[2 * kPPRows + local_row] = vs_ref;
-    }
-}
-
-// ---------------------------------------------------------------- INT8 prefill, one wave per SIMD
+// ---------------------------------------------------------------- prefill, one wave per SIMD
 //
 // A work-group of 4 waves (one per SIMD, up to 512 registers each) owns 256 logical rows of one
-// KV group, as prefill_pp_kernel; wave w owns rows 64w .. 64w + 63 as two 32-row blocks, so every
-// K or V operand read from LDS feeds two MFMAs, its query stays in registers and its O^T
-// accumulators fill the accumulator registers. A single wave overlaps its own VALU work with its
-// MFMAs: an MFMA occupies the matrix pipe for ~32 cycles while the wave issues independent VALU
-// instructions beside it (about six per MFMA come free). Each 32-key tile n runs in two phases:
-//   A: S(n) = K(n) Q^T for both row blocks (32 MFMAs), interleaved with the INT8 -> FP16 staging
-//      of tile n + 1 and the loads of tile n + 2;
-//   B: O += V(n - 1)^T P(n - 1) for both row blocks (32 MFMAs), interleaved with the online
-//      softmax of S(n), which produces P(n).
-// One work-group barrier per tile, between the phases. K tiles are double-buffered and V tiles
-// (with the tile's scales) quadruple-buffered, so that a buffer written in phase A of tile n
-// was last read before the barrier of tile n - 1 and the operand reads of the next phase never
-// wait for a barrier: tile n + 1's K operands are read ahead during phase B of tile n.
+// KV group and walks its key range in 32-key tiles; wave w owns rows 64w .. 64w + 63 as two
+// 32-row blocks, so every K or V operand read from LDS feeds two MFMAs, most of its query stays
+// in registers and its O^T accumulators fill the accumulator registers. The wave overlaps its
+// own vector work with its MFMAs: an MFMA occupies the matrix pipe for ~32 cycles while the wave
+// issues independent VALU instructions beside it (about six per MFMA come free). Tile n runs in
+// two phases, one work-group barrier apart:
+//   A: S(n) = K(n) Q^T for both row blocks (32 MFMAs), interleaved with the exponentials of
+//      tile n - 1 (P(n - 1), FP16, and l);
+//   B: O += V(n - 1)^T P(n - 1) (32 MFMAs), interleaved with S(n)'s scaling and row maxima, the
+//      staging of tile n + 2 (INT8: codes converted to FP16; FP16: copied, V transposed) and
+//      the loads of tile n + 3.
+// Rows whose maximum grows by more than 2^8, and tiles on the causal diagonal, take a fix-up
+// after phase B (the general softmax); the common case needs no maximum before exp2. The
+// MFMAs are inline assembly, so that their order, and the operand reads placed three steps
+// ahead of them, are kept; each step's vector work is tied behind its MFMA. K tiles are
+// double-buffered and V tiles (with the tile's scales) quadruple-buffered: every buffer a
+// phase writes was last read before the previous barrier.
 constexpr int kW64Keys = 32;               // keys per tile
 constexpr int kW64VBufs = 4;               // V^T tiles in LDS
 #ifndef BOOT_W64_QLDS
@@ -737,6 +165,7 @@ struct W64VTile {
     float vs[kW64Keys];                    // V scale / vs_ref (0 beyond K)
 };
 
+template <bool kInt8>
 __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
     __shared__ W64KTile kbuf[2];
     __shared__ W64VTile vbuf[kW64VBufs];
@@ -762,7 +191,7 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: wave-level branches stay scalar
     const int i = lane & 31, kk = lane >> 5;
     const uint32_t R = p.rows * 8;
-    const uint32_t r0 = tile * kPPRows + 64 * wave;          // first row of this wave
+    const uint32_t r0 = tile * kTileRows + 64 * wave;          // first row of this wave
     uint32_t my_row[2], limit[2];
     bool row_valid[2];
 #pragma unroll
@@ -771,7 +200,7 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
         row_valid[rb] = my_row[rb] < R;
         limit[rb] = p.pos + (row_valid[rb] ? my_row[rb] : R - 1) / 8;   // keys <= limit visible
     }
-    const uint32_t tile_last = min(R - 1, tile * kPPRows + kPPRows - 1);
+    const uint32_t tile_last = min(R - 1, tile * kTileRows + kTileRows - 1);
     const uint32_t tile_end = p.pos + tile_last / 8 + 1;               // keys [0, tile_end)
     const uint32_t kbeg = split * p.split_keys;
     const uint32_t kend = min(tile_end, kbeg + p.split_keys);
@@ -779,52 +208,110 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
     const uint32_t wave_min_limit = p.pos + min(R - 1, r0) / 8;
     const uint32_t last_key0 = kbeg + (uint32_t)max(ntiles - 1, 0) * kW64Keys;   // loads never go past it
 
-    // ---- staging: thread t converts 32 K codes (rows krow0 and krow0 + 4, 16 codes at
-    // 16 * kchunk; a load instruction reads four whole 256-byte rows) and the 32 V codes of
-    // page row t; threads t < 32 carry the scales of key t
-    const int8_t *kcodes = (const int8_t *)p.k;
-    const int8_t *vcodes = (const int8_t *)p.v;
-    const int krow0 = 8 * wave + (lane >> 4), kchunk = lane & 15;
-    uint4 rk0, rk1, rv0, rv1;
-    float pre_ks = 0.0f, pre_vs = 0.0f;
+    // ---- staging. INT8: thread t converts 32 K codes (rows krow0 and krow0 + 4, 16 codes at
+    // 16 * kchunk; a load instruction reads four whole 256-byte rows) and the 32 V codes of page
+    // row t (V pages are already dimension-major). FP16: thread t copies 16-byte pieces of K rows
+    // 4 (t / 32) + j (piece t % 32; a load reads two whole 512-byte rows) and transposes a block of
+    // 4 keys (4 (t / 32) + r) x 8 dimensions (8 (t % 32) + e) of the key-major V into V^T.
+    const int krow0 = 8 * wave + (lane >> 4), kchunk = lane & 15;   // INT8 K
+    const int fgroup = tid >> 5, fpiece = tid & 31;                 // FP16 K rows / V keys, piece
+    struct Raw {
+        uint4 w[8];    // INT8: K rows krow0, krow0 + 4, V page row t; FP16: 4 K pieces, 4 V keys
+        float ks, vs;  // INT8: scales of key t % 32
+    };
     auto load_raw = [&](uint32_t key0) __attribute__((always_inline)) {
+        Raw r;
         key0 = min(key0, last_key0);
-        const uint32_t ka = min(key0 + (uint32_t)krow0, p.keys - 1), kb2 = min(key0 + (uint32_t)krow0 + 4, p.keys - 1);
-        rk0 = *reinterpret_cast<const uint4 *>(kcodes + (size_t)((ka * 2 + g) * 256 + kchunk * 16));
-        rk1 = *reinterpret_cast<const uint4 *>(kcodes + (size_t)((kb2 * 2 + g) * 256 + kchunk * 16));
-        const size_t offv = (size_t)value_index((uint64_t)key0 * 2 + g, 0) + (size_t)tid * 256;
-        rv0 = *reinterpret_cast<const uint4 *>(vcodes + offv);
-        rv1 = *reinterpret_cast<const uint4 *>(vcodes + offv + 16);
-        const size_t at = (size_t)min(key0 + (uint32_t)(tid & 31), p.keys - 1) * 2 + g;
-        pre_ks = p.ks[at];
-        pre_vs = p.vs[at];
+        if constexpr (kInt8) {
+            const int8_t *kcodes = (const int8_t *)p.k, *vcodes = (const int8_t *)p.v;
+            const uint32_t ka = min(key0 + (uint32_t)krow0, p.keys - 1), kb2 = min(key0 + (uint32_t)krow0 + 4, p.keys - 1);
+            r.w[0] = *reinterpret_cast<const uint4 *>(kcodes + (size_t)((ka * 2 + g) * 256 + kchunk * 16));
+            r.w[1] = *reinterpret_cast<const uint4 *>(kcodes + (size_t)((kb2 * 2 + g) * 256 + kchunk * 16));
+            const size_t offv = (size_t)value_index((uint64_t)key0 * 2 + g, 0) + (size_t)tid * 256;
+            r.w[2] = *reinterpret_cast<const uint4 *>(vcodes + offv);
+            r.w[3] = *reinterpret_cast<const uint4 *>(vcodes + offv + 16);
+            const size_t at = (size_t)min(key0 + (uint32_t)(tid & 31), p.keys - 1) * 2 + g;
+            r.ks = p.ks[at];
+            r.vs = p.vs[at];
+        } else {
+            // keys past K are clamped to K - 1: the cache beyond K (NaN padding) is never read
+            const _Float16 *kh = (const _Float16 *)p.k, *vh = (const _Float16 *)p.v;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t key = min(key0 + (uint32_t)(4 * fgroup + j), p.keys - 1);
+                r.w[j] = *reinterpret_cast<const uint4 *>(kh + ((size_t)key * 2 + g) * 256 + 8 * fpiece);
+                r.w[4 + j] = *reinterpret_cast<const uint4 *>(vh + ((size_t)key * 2 + g) * 256 + 8 * fpiece);
+            }
+            r.ks = r.vs = 0.0f;
+        }
+        return r;
     };
     float vs_inv = 0.0f;
-    // Staging in pieces, so that phase A can spread them between its MFMAs. Piece j < 4 converts
-    // and writes 8 K codes, piece 4 <= j < 8 8 V codes; every wave writes the tile's scales (the
-    // same values from each wave: lane l carries key l % 32).
+    // Staging in pieces, so that phase B can spread them between its MFMAs. Piece j < 4 writes K
+    // (INT8: 8 converted codes; FP16: a copied 16-byte piece), piece 4 <= j < 8 V (INT8: 8
+    // converted codes; FP16: dimensions 2 (j - 4) and 2 (j - 4) + 1 of the 4 keys). Every wave
+    // writes the tile's scales (the same values from each wave: lane l carries key l % 32).
     const int vsw_stage = (tid >> 2) & 3;
-    auto stage_piece = [&](W64KTile &kb, W64VTile &vb, int j) __attribute__((always_inline)) {
-        const uint4 &r = j < 2 ? rk0 : j < 4 ? rk1 : j < 6 ? rv0 : rv1;
-        const uint32_t lo = (j & 1) ? r.z : r.x, hi = (j & 1) ? r.w : r.y;
-        uint4 h;
-        i8x4_to_f16(lo, h.x, h.y);
-        i8x4_to_f16(hi, h.z, h.w);
-        if (j < 4)
-            *reinterpret_cast<uint4 *>(kb.k + (krow0 + 4 * (j >> 1)) * kKStride + kchunk * 16 + 8 * (j & 1)) = h;
-        else
-            *reinterpret_cast<uint4 *>(vb.v + tid * kW64Keys + 8 * ((j - 4) ^ vsw_stage)) = h;
+    auto piece_words = [&](const Raw &r, int j, uint32_t (&x)[4]) __attribute__((always_inline)) {
+        if constexpr (kInt8) {
+            const uint4 &w = r.w[j >> 1];
+            x[0] = (j & 1) ? w.z : w.x;
+            x[1] = (j & 1) ? w.w : w.y;
+            x[2] = x[3] = 0;
+        } else if (j < 4) {
+            x[0] = r.w[j].x;
+            x[1] = r.w[j].y;
+            x[2] = r.w[j].z;
+            x[3] = r.w[j].w;
+        } else {
+            const int d = j - 4;   // dword d of each key: dimensions 8 fpiece + 2d, + 1
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint4 &w = r.w[4 + k];
+                x[k] = d == 0 ? w.x : d == 1 ? w.y : d == 2 ? w.z : w.w;
+            }
+        }
     };
-    auto stage_scales = [&](W64VTile &vb, uint32_t key0) __attribute__((always_inline)) {
+    auto stage_piece = [&](W64KTile &kb, W64VTile &vb, int j, const uint32_t (&x)[4]) __attribute__((always_inline)) {
+        if constexpr (kInt8) {
+            uint4 h;
+            i8x4_to_f16(x[0], h.x, h.y);
+            i8x4_to_f16(x[1], h.z, h.w);
+            if (j < 4)
+                *reinterpret_cast<uint4 *>(kb.k + (krow0 + 4 * (j >> 1)) * kKStride + kchunk * 16 + 8 * (j & 1)) = h;
+            else
+                *reinterpret_cast<uint4 *>(vb.v + tid * kW64Keys + 8 * ((j - 4) ^ vsw_stage)) = h;
+        } else if (j < 4) {
+            *reinterpret_cast<uint4 *>(kb.k + (4 * fgroup + j) * kKStride + 8 * fpiece) = make_uint4(x[0], x[1], x[2], x[3]);
+        } else {
+            // keys 4 fgroup .. + 3 of V^T rows e and e + 1: 8 bytes each, in the 16-byte piece
+            // fgroup / 2 (XOR-swizzled by the row as the operand reads expect)
+            const int e = 8 * fpiece + 2 * (j - 4);
+            const uint2 lo = make_uint2(__builtin_amdgcn_perm(x[1], x[0], 0x05040100u), __builtin_amdgcn_perm(x[3], x[2], 0x05040100u));
+            const uint2 hi = make_uint2(__builtin_amdgcn_perm(x[1], x[0], 0x07060302u), __builtin_amdgcn_perm(x[3], x[2], 0x07060302u));
+            *reinterpret_cast<uint2 *>(vb.v + e * kW64Keys + 8 * ((fgroup >> 1) ^ ((e >> 2) & 3)) + 4 * (fgroup & 1)) = lo;
+            *reinterpret_cast<uint2 *>(vb.v + (e + 1) * kW64Keys + 8 * ((fgroup >> 1) ^ (((e + 1) >> 2) & 3)) + 4 * (fgroup & 1)) = hi;
+        }
+    };
+    auto stage_scales = [&](W64VTile &vb, uint32_t key0, const Raw &r) __attribute__((always_inline)) {
         const int t = tid & 31;
         const bool inside = key0 + t < p.keys;   // poisoned tails beyond K never reach S or P
-        vb.ks[t] = inside ? pre_ks * (kLog2e / 16.0f) : 0.0f;
-        vb.vs[t] = inside ? pre_vs * vs_inv : 0.0f;
+        if constexpr (kInt8) {
+            vb.ks[t] = inside ? r.ks * (kLog2e / 16.0f) : 0.0f;
+            vb.vs[t] = inside ? r.vs * vs_inv : 0.0f;
+        } else {
+            vb.ks[t] = inside ? kLog2e / 16.0f : 0.0f;
+            vb.vs[t] = inside ? 1.0f : 0.0f;
+        }
     };
-    auto stage = [&](W64KTile &kb, W64VTile &vb, uint32_t key0) __attribute__((always_inline)) {
+    auto stage = [&](W64KTile &kb, W64VTile &vb, uint32_t key0, const Raw &r) __attribute__((always_inline)) {
 #pragma unroll
-        for (int j = 0; j < 8; j++) stage_piece(kb, vb, j);
-        stage_scales(vb, key0);
+        for (int j = 0; j < 8; j++) {
+            uint32_t x[4];
+            piece_words(r, j, x);
+            stage_piece(kb, vb, j, x);
+        }
+        stage_scales(vb, key0, r);
     };
 
     // ---- prologue: the V scales of the split (vs_ref), tile 0's codes, the query
@@ -832,9 +319,9 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
 #pragma unroll
     for (int it = 0; it < 8; it++) {
         const uint32_t key = kbeg + tid + 256 * it;
-        vsv[it] = key < kend ? p.vs[(size_t)key * 2 + g] : 0.0f;
+        vsv[it] = kInt8 && key < kend ? p.vs[(size_t)key * 2 + g] : 0.0f;
     }
-    load_raw(kbeg);
+    const Raw raw0 = load_raw(kbeg), raw1 = load_raw(kbeg + kW64Keys);
     half8 qop[2][kW64QRegs];
 #pragma unroll
     for (int rb = 0; rb < 2; rb++) {
@@ -845,10 +332,11 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
 #pragma unroll
         for (int c = kW64QRegs; c < 16; c++) qlds[c - kW64QRegs][rb][tid] = *reinterpret_cast<const uint4 *>(qrow + 16 * c);
     }
-    float vs_ref = 0.0f;
+    float vs_ref = kInt8 ? 0.0f : 1.0f;   // FP16 KV: no V scales
 #pragma unroll
     for (int it = 0; it < 8; it++) vs_ref = fmaxf(vs_ref, vsv[it]);
-    for (uint32_t key = kbeg + tid + 2048; key < kend; key += 256) vs_ref = fmaxf(vs_ref, p.vs[(size_t)key * 2 + g]);
+    if (kInt8)
+        for (uint32_t key = kbeg + tid + 2048; key < kend; key += 256) vs_ref = fmaxf(vs_ref, p.vs[(size_t)key * 2 + g]);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) vs_ref = fmaxf(vs_ref, __shfl_xor(vs_ref, o, 64));
     if (lane == 0) vs_partial[wave] = vs_ref;
@@ -857,8 +345,9 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
     vs_ref = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, vs_ref)));
     vs_inv = __builtin_bit_cast(
         float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, vs_ref > 0.0f ? 1.0f / vs_ref : 0.0f)));
-    stage(kbuf[0], vbuf[0], kbeg);
-    load_raw(kbeg + kW64Keys);
+    stage(kbuf[0], vbuf[0], kbeg, raw0);
+    stage(kbuf[1], vbuf[1], kbeg + kW64Keys, raw1);
+    Raw raw = load_raw(kbeg + 2 * kW64Keys);   // staged in phase B of tile 0
     {
         // "tile -1", whose zero probabilities the first PV multiplies: zero V^T codes and scales,
         // not NaN
@@ -907,11 +396,10 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
         lsum[rb] += e;
     };
 
-    // Phase A of tile n: S(n) for both row blocks (K operands read three steps ahead), the staging
-    // of tile n + 1, the loads of tile n + 2 and the exponentials of tile n - 1 (P(n - 1) and l),
-    // spread between the MFMAs. One path for every n: after the last tile (n = ntiles) the
-    // MFMAs multiply the finite codes staged for keys past the split, an S that phase B replaces
-    // with -inf, and the staging fills buffers no later phase reads.
+    // Phase A of tile n: S(n) for both row blocks (K operands read three steps ahead) and the
+    // exponentials of tile n - 1 (P(n - 1) and l), spread between the MFMAs. One path for every
+    // n: after the last tile (n = ntiles) the MFMAs multiply the finite codes staged for keys past
+    // the split, an S that phase B replaces with -inf.
     auto phase_a = [&](int n, floatx16 (&sc)[2], floatx16 (&sp)[2], const float (&dec)[2], half8 (&pn)[2][2])
         __attribute__((always_inline)) {
         float4 v4[4];
@@ -919,9 +407,6 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
         float lsum[2] = {0.0f, 0.0f};
         {
             const _Float16 *kr = kbuf[n & 1].k + qk_key_row(i) * kKStride + 8 * kk;
-            const uint32_t next0 = kbeg + (uint32_t)(n + 1) * kW64Keys;
-            W64KTile &kdst = kbuf[(n + 1) & 1];                 // past the last tile: unread buffers
-            W64VTile &vdst = vbuf[(n + 1) % kW64VBufs];
             half8 kop[4];                                       // K operands, read three steps ahead
             half8 qop_l[4][2];                                  // Q^T chunks from LDS, likewise
 #pragma unroll
@@ -949,16 +434,9 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
                 {
                     // this step's inputs follow the MFMA, the previous step's row sum precedes it
                     float z = sp[0][c];
-                    if (c < 8) {
-                        uint4 &r = c < 2 ? rk0 : c < 4 ? rk1 : c < 6 ? rv0 : rv1;
-                        after_mfma((c & 1) ? r.z : r.x, (c & 1) ? r.w : r.y, z, lsum[1]);
-                    } else {
-                        after_mfma(z, lsum[1]);
-                    }
+                    after_mfma(z, lsum[1]);
                     sp[0][c] = z;
                 }
-                if (c < 8) stage_piece(kdst, vdst, c);          // staging of tile n + 1
-                if (c == 8) stage_scales(vdst, next0);
                 exp_elem(0, c, sp, v4, pn, lsum);
                 if (c == 0)
                     s_mfma_first(sc[1], kop[c & 3], q1);
@@ -972,7 +450,6 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
                     sp[1][c] = z;
                 }
                 exp_elem(1, c, sp, v4, pn, lsum);
-                if (c == 9) load_raw(next0 + kW64Keys);       // the codes of tile n + 2
             }
         }
 #pragma unroll
@@ -996,8 +473,11 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
     // first key): fix_softmax handles those and the causal mask. One code path for every tile (the
     // accumulators must not meet branches): before the first tile P is zero and the V buffer it
     // reads is zero-filled; after the last (past), S is -inf, which leaves m, l and P unchanged.
-    auto phase_b = [&](int n, floatx16 (&sc)[2], const half8 (&pp)[2][2], bool (&need)[2], float (&ymax)[2], bool past)
-        __attribute__((always_inline)) {
+    auto phase_b = [&](int n, floatx16 (&sc)[2], const half8 (&pp)[2][2], bool (&need)[2], float (&ymax)[2], bool past,
+                       Raw &raw) __attribute__((always_inline)) {
+        const uint32_t key2 = kbeg + (uint32_t)(n + 2) * kW64Keys;
+        W64KTile &kdst = kbuf[n & 1];                 // tile n's, read in phase A of tile n
+        W64VTile &vdst = vbuf[(n + 2) % kW64VBufs];   // tile n - 2's, read in phase B of tile n - 1
         float4 k4[4];
         load_scales(n, false, k4);
         float add[2];
@@ -1038,17 +518,31 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
             o_mfma(o[0][j & 7], va, pp[0][j >> 3]);
             if (j < 8) scale_pair(0, j);
             else max_piece(0, j);
+            if (j >= 4 && j < 12) {   // staging of tile n + 2 (past the split: buffers no phase reads)
+                uint32_t x[4];
+                piece_words(raw, j - 4, x);
+                if (kInt8)
+                    after_mfma(x[0], x[1]);
+                else
+                    after_mfma(x[0], x[1], x[2], x[3]);
+                stage_piece(kdst, vdst, j - 4, x);
+            }
+            if (j == 12) stage_scales(vdst, key2, raw);
             o_mfma(o[1][j & 7], va, pp[1][j >> 3]);
             if (j < 8) scale_pair(1, j);
             else max_piece(1, j);
+            if (j == 13) raw = load_raw(key2 + kW64Keys);   // the codes of tile n + 3
         }
     };
 
     // The general case of tile n, after phase B: the causal mask, the lazy running maximum (a row
     // rebases only when its maximum grows by more than 2^8, so exponentials stay <= 256): S is
     // shifted by the rebase, `dec` is the factor l takes before tile n's sum joins it.
-    auto fix_softmax = [&](int n, floatx16 (&sc)[2], float (&ymax)[2], float (&dec)[2], bool masked)
-        __attribute__((always_inline)) {
+    // `rescale_row` reports the rows whose O must take dec: a rebase of a row that had keys before.
+    // A row's first rebase finds O zero; any other takes dec, also where exp2(-ymax) underflows to 0
+    // (a maximum that grows by more than 2^149 leaves nothing of the earlier keys).
+    auto fix_softmax = [&](int n, floatx16 (&sc)[2], float (&ymax)[2], float (&dec)[2], bool (&rescale_row)[2],
+                           bool masked) __attribute__((always_inline)) {
         const uint32_t key0 = kbeg + (uint32_t)n * kW64Keys;
         if (masked) {
 #pragma unroll
@@ -1064,6 +558,7 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
             const bool rebase = ymax[rb] > 8.0f || (m[rb] == -INFINITY && ymax[rb] > -INFINITY);
             const float mref = m[rb] == -INFINITY ? 0.0f : m[rb];
             dec[rb] = rebase ? (m[rb] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(-ymax[rb])) : 1.0f;
+            rescale_row[rb] = rebase && m[rb] != -INFINITY;
             m[rb] = rebase ? mref + ymax[rb] : m[rb];
             if (rebase) {
 #pragma unroll
@@ -1112,14 +607,15 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
         __syncthreads();
         bool need[2];
         float ymax[2];
-        phase_b(n, sc, pb, need, ymax, n == ntiles);
+        phase_b(n, sc, pb, need, ymax, n == ntiles, raw);
         dec[0] = dec[1] = 1.0f;
         const bool masked = kbeg + (uint32_t)n * kW64Keys + kW64Keys - 1 > wave_min_limit;
         if (masked | (__ballot(need[0] | need[1]) != 0)) {   // bitwise: both sides computed
-            fix_softmax(n, sc, ymax, dec, masked);
-            // a rebase scales what O holds (through tile n - 1) before P(n) joins it; the first
-            // rebase of a row finds O zero
-            if (__ballot((dec[0] != 1.0f && dec[0] != 0.0f) || (dec[1] != 1.0f && dec[1] != 0.0f))) rescale(dec);
+            bool rescale_row[2];
+            fix_softmax(n, sc, ymax, dec, rescale_row, masked);
+            // a rebase scales what O holds (through tile n - 1) before P(n) joins it (rows that do
+            // not rebase take dec = 1; a first rebase, dec = 0, finds O zero)
+            if (__ballot(rescale_row[0] | rescale_row[1])) rescale(dec);
         }
 #pragma unroll
         for (int rb = 0; rb < 2; rb++) sp[rb] = sc[rb];
@@ -1164,7 +660,7 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
                             : wave == 2 ? reinterpret_cast<unsigned char *>(&vbuf[2])
                                         : reinterpret_cast<unsigned char *>(qlds);
     unsigned char *pbase = reinterpret_cast<unsigned char *>(p.partial) +
-                           (((size_t)g * p.tiles + tile) * p.splits + split) * kPPPartialBytes;
+                           (((size_t)g * p.tiles + tile) * p.splits + split) * kPartialBytes;
     typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 #pragma unroll
     for (int rb = 0; rb < 2; rb++) {
@@ -1181,10 +677,10 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
             }
         if (kk == 0) {
             const int local_row = 64 * wave + row;
-            float *stat = reinterpret_cast<float *>(pbase + (size_t)kPPRows * 256 * 2);
+            float *stat = reinterpret_cast<float *>(pbase + (size_t)kTileRows * 256 * 2);
             stat[local_row] = m[rb];
-            stat[kPPRows + local_row] = l[rb];
-            stat[2 * kPPRows + local_row] = vs_ref;
+            stat[kTileRows + local_row] = l[rb];
+            stat[2 * kTileRows + local_row] = vs_ref;
         }
     }
     unsigned char *pw = pbase + (size_t)(64 * wave) * 512;   // the wave's rows are contiguous
@@ -1196,76 +692,16 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
     }
 }
 
-// Merges the split partials (O^T scaled by vs_ref, m, l in base 2): one wave per
-// logical row, four dimensions per lane, eight splits per step with all their loads
-// in flight together and a running maximum across steps, so a chunk with at most
-// eight splits makes one memory round trip.
-template <int kTileRows>
-__global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillParams p) {
-    constexpr size_t kStride = (size_t)kTileRows * 256 + 2 * kTileRows;
-    const uint32_t lane = threadIdx.x & 63;
-    const uint32_t local_row = blockIdx.x * 4 + (threadIdx.x >> 6), tile = blockIdx.y, g = blockIdx.z;
-    const uint32_t row = tile * kTileRows + local_row;
-    if (row >= p.rows * 8) return;   // wave-uniform
-    const float *base = p.partial + ((size_t)g * p.tiles + tile) * p.splits * kStride;
-    const uint32_t token = row / 8, head = g * 8 + row % 8;
-    const size_t at = ((size_t)token * 16 + head) * 256 + 4 * lane;
-    const float4 gv = *reinterpret_cast<const float4 *>(p.gate + at);
-    float mrun = -INFINITY, lsum = 0.0f;
-    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (uint32_t s0 = 0; s0 < p.splits; s0 += 8) {
-        float ms[8], ls[8];
-        float4 os[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const uint32_t s = min(s0 + j, p.splits - 1);
-            const float *part = base + s * kStride;
-            ms[j] = s0 + j < p.splits ? part[(size_t)kTileRows * 256 + local_row] : -INFINITY;
-            ls[j] = part[(size_t)kTileRows * 256 + kTileRows + local_row];
-            os[j] = *reinterpret_cast<const float4 *>(part + (size_t)local_row * 256 + 4 * lane);
-        }
-        float mstep = ms[0];
-#pragma unroll
-        for (int j = 1; j < 8; j++) mstep = fmaxf(mstep, ms[j]);
-        if (mstep == -INFINITY) continue;   // wave-uniform: every split of the step is empty
-        const float mnew = fmaxf(mrun, mstep);
-        const float decay = mrun == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mrun - mnew);
-        mrun = mnew;
-        lsum *= decay;
-        acc.x *= decay;
-        acc.y *= decay;
-        acc.z *= decay;
-        acc.w *= decay;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            if (ms[j] == -INFINITY) continue;
-            const float f = __builtin_amdgcn_exp2f(ms[j] - mnew);
-            lsum += ls[j] * f;
-            acc.x += os[j].x * f;
-            acc.y += os[j].y * f;
-            acc.z += os[j].z * f;
-            acc.w += os[j].w * f;
-        }
-    }
-    const float inv = 1.0f / lsum;
-    float4 out;
-    out.x = acc.x * inv * sigmoidf(gv.x);
-    out.y = acc.y * inv * sigmoidf(gv.y);
-    out.z = acc.z * inv * sigmoidf(gv.z);
-    out.w = acc.w * inv * sigmoidf(gv.w);
-    *reinterpret_cast<float4 *>(p.y + at) = out;
-}
-
-// Merges the FP16 split partials of prefill_pp_kernel (O^T / l, then m, l, vs_ref per
+// Merges the FP16 split partials of prefill_w64_kernel (O^T / l, then m, l, vs_ref per
 // row): one wave per logical row, four dimensions per lane, eight splits per step with
 // a running maximum, as prefill_combine_kernel.
 __global__ __launch_bounds__(256) void prefill_combine_half_kernel(PrefillParams p) {
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t local_row = blockIdx.x * 4 + (threadIdx.x >> 6), tile = blockIdx.y, g = blockIdx.z;
-    const uint32_t row = tile * kPPRows + local_row;
+    const uint32_t row = tile * kTileRows + local_row;
     if (row >= p.rows * 8) return;   // wave-uniform
     const unsigned char *base = reinterpret_cast<const unsigned char *>(p.partial) +
-                                ((size_t)g * p.tiles + tile) * p.splits * kPPPartialBytes;
+                                ((size_t)g * p.tiles + tile) * p.splits * kPartialBytes;
     const uint32_t token = row / 8, head = g * 8 + row % 8;
     const size_t at = ((size_t)token * 16 + head) * 256 + 4 * lane;
     const float4 gv = *reinterpret_cast<const float4 *>(p.gate + at);
@@ -1278,11 +714,11 @@ __global__ __launch_bounds__(256) void prefill_combine_half_kernel(PrefillParams
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const uint32_t s = min(s0 + j, p.splits - 1);
-            const unsigned char *part = base + s * kPPPartialBytes;
-            const float *stat = reinterpret_cast<const float *>(part + (size_t)kPPRows * 256 * 2);
+            const unsigned char *part = base + s * kPartialBytes;
+            const float *stat = reinterpret_cast<const float *>(part + (size_t)kTileRows * 256 * 2);
             ms[j] = s0 + j < p.splits ? stat[local_row] : -INFINITY;
-            ls[j] = stat[kPPRows + local_row];
-            ws[j] = stat[2 * kPPRows + local_row];
+            ls[j] = stat[kTileRows + local_row];
+            ws[j] = stat[2 * kTileRows + local_row];
             os[j] = *reinterpret_cast<const half4 *>(reinterpret_cast<const _Float16 *>(part) + (size_t)local_row * 256 + 4 * lane);
         }
         float mstep = ms[0];
@@ -1356,20 +792,17 @@ const char *launch_prefill(Context &c, const View *b, const boot_kernel_args &a,
     p.rows = (uint32_t)rows;
     p.pos = a.pos;
     p.keys = (uint32_t)keys;
-    // INT8: 256-row work-groups of 8 waves, one per CU; FP16 control: 128-row
-    // work-groups of 4 waves, two per CU.
-    const uint64_t tile_rows = int8 ? kPPRows : kRows;
-    const uint64_t tile_keys = int8 ? kPPKeys : kKeys;
-    const uint64_t per_cu = int8 ? 1 : 2;
-    const size_t stride_bytes = int8 ? kPPPartialBytes : kPartialStride * sizeof(float);
-    p.tiles = (uint32_t)((rows * 8 + tile_rows - 1) / tile_rows);
+    // 256-row work-groups of 4 waves (one per SIMD), one per CU, for both storage formats: the
+    // FP16-KV control runs the same schedule with FP16 staging, so that the two differ only in
+    // the cache they read.
+    p.tiles = (uint32_t)((rows * 8 + kTileRows - 1) / kTileRows);
     // split-K: enough blocks to fill the CUs, each split at least 256 keys
     const uint64_t base_blocks = 2ull * p.tiles;
-    const uint64_t want = per_cu * (uint64_t)std::max(1, context_cus(c));
+    const uint64_t want = (uint64_t)std::max(1, context_cus(c));
     uint64_t splits = std::max<uint64_t>(1, (want + base_blocks - 1) / base_blocks);
     splits = std::min<uint64_t>(splits, std::max<uint64_t>(1, keys / 256));
     uint64_t split_keys = (keys + splits - 1) / splits;
-    split_keys = (split_keys + tile_keys - 1) / tile_keys * tile_keys;
+    split_keys = (split_keys + kW64Keys - 1) / kW64Keys * kW64Keys;
     splits = (keys + split_keys - 1) / split_keys;
     p.splits = (uint32_t)splits;
     p.split_keys = (uint32_t)split_keys;
@@ -1377,24 +810,16 @@ const char *launch_prefill(Context &c, const View *b, const boot_kernel_args &a,
     p.remap = ((2 * splits) % 8 == 0) ? 1u : 0u;
     p.partial = nullptr;
     if (splits > 1) {
-        p.partial = (float *)context_workspace(c, base_blocks * splits * stride_bytes);
+        p.partial = (float *)context_workspace(c, base_blocks * splits * kPartialBytes);
         BOOT_REQUIRE(p.partial, "cannot allocate prefill split workspace");
     }
-#ifdef BOOT_PREFILL_PP
     if (int8)
-        launch_timed(c, "prefill_pp_kernel", prefill_pp_kernel, dim3((uint32_t)blocks), dim3(512), p);
-#else
-    if (int8)
-        launch_timed(c, "prefill_w64_kernel", prefill_w64_kernel, dim3((uint32_t)blocks), dim3(256), p);
-#endif
+        launch_timed(c, "prefill_w64_kernel", prefill_w64_kernel<true>, dim3((uint32_t)blocks), dim3(256), p);
     else
-        launch_timed(c, "prefill_fp16_kernel", prefill_fp16_kernel, dim3((uint32_t)blocks), dim3(256), p);
+        launch_timed(c, "prefill_w64_fp16_kernel", prefill_w64_kernel<false>, dim3((uint32_t)blocks), dim3(256), p);
     if (splits > 1) {
         context_split(c, int8 ? "attention_online_int8.combine" : "attention_online_fp16.combine");
-        if (int8)
-            launch_timed(c, "prefill_combine_half_kernel", prefill_combine_half_kernel, dim3(kPPRows / 4, p.tiles, 2), dim3(256), p);
-        else
-            launch_timed(c, "prefill_combine_kernel<128>", prefill_combine_kernel<kRows>, dim3(kRows / 4, p.tiles, 2), dim3(256), p);
+        launch_timed(c, "prefill_combine_half_kernel", prefill_combine_half_kernel, dim3(kTileRows / 4, p.tiles, 2), dim3(256), p);
     }
     return nullptr;
 }

@@ -70,6 +70,25 @@ def test_prefill_matches_fp64(device, oracle, history, rows):
     cache.dispose()
 
 
+@pytest.mark.parametrize("history,rows", [(0, 1), (17, 7), (127, 33), (257, 64), (8192, 128), (3584, 512)])
+def test_prefill_stress_x16(device, oracle, history, rows):
+    """The stress mode of OnlineAttentionTests.cs:28 on the INT8 cache: Q and K x16 (K's codes
+    are unchanged, its scales x16), logits x256 and near one-hot rows, which rebase often."""
+    k, v = reference_kv(history + rows)
+    q, gate, host = build_case(oracle, history, rows, kv=(k * np.float32(16), v))
+    q = q * np.float32(16)
+    cache = upload_cache(device, *host)
+    y = run_prefill(device, q, gate, cache, rows, history)
+    assert np.isnan(y[-1])
+    y = y[:-1]
+    assert np.all(np.isfinite(y))
+    ref, bound = oracle.attention(q, *host, gate, rows, history, round_q_half=1, with_bound=True)
+    err = np.abs(y - ref)
+    assert rel_l2(y, ref) <= REL_L2 and err.max() <= MAX_ABS, (rel_l2(y, ref), err.max())
+    assert np.all(err <= bound / 256 + 1e-4)
+    cache.dispose()
+
+
 @pytest.mark.parametrize("slope", [0.05, 0.6])
 def test_prefill_rising_scores(device, oracle, slope):
     """Scores that rise along the keys by about `slope` (natural log) per token: the online

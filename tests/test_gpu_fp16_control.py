@@ -35,13 +35,19 @@ def test_batch_rope_fp16_storage(device, oracle):
         b.dispose()
 
 
-@pytest.mark.parametrize("history,rows", [(0, 1), (17, 7), (127, 33), (257, 64), (4093, 7), (8192, 128), (3584, 512),
-                                          (30208, 512)])
-def test_online_fp16_matches_fp64(device, oracle, history, rows):
+CASES = [(0, 1), (17, 7), (127, 33), (257, 64), (4093, 7), (8192, 128), (3584, 512), (30208, 512)]
+# the stress mode of OnlineAttentionTests.cs:28: Q and K x16 (logits x256, near one-hot rows)
+STRESS = [(0, 1), (17, 7), (127, 33), (257, 64), (8192, 128), (3584, 512)]
+
+
+@pytest.mark.parametrize("history,rows,stress", [c + (False,) for c in CASES] + [c + (True,) for c in STRESS])
+def test_online_fp16_matches_fp64(device, oracle, history, rows, stress):
     length = history + rows
     k = oracle.fill_hash(length * 512, 31, 3)       # OnlineAttentionTests.cs:26-27 fills
     v = oracle.fill_hash(length * 512, 23, 1)
     q = oracle.fill_hash(rows * 4096, 17, 3)
+    if stress:
+        q, k = q * np.float32(16), k * np.float32(16)
     gate = oracle.fill_hash(rows * 4096, 11, 1)
     kh = np.full((length + 128) * 512, np.nan, np.float16)    # NaN padding (OnlineAttentionTests.cs:29)
     vh = np.full((length + 128) * 512, np.nan, np.float16)
