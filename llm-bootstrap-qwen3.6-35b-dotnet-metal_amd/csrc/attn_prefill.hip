@@ -68,6 +68,14 @@ __device__ inline float sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }
 // Key row of QK tile row i: bits 2 and 3 of i swapped (see header comment).
 __device__ inline int qk_key_row(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
 
+// v_max3_f32 without the canonicalizing moves the compiler adds in front of
+// fmaxf when it cannot prove its inputs canonical (no NaN reaches this kernel).
+__device__ inline float max3f(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
 // Max over the lane pair (l, l ^ 32). v_permlane32_swap exchanges lanes 32-63 of
 // its first operand with lanes 0-31 of its second, so with both holding x every
 // lane ends with its own value in one register and its partner's in the other.
@@ -77,16 +85,9 @@ __device__ inline int qk_key_row(int i) { return (i & ~12) | ((i & 4) << 1) | ((
 __device__ inline float pair_max(float x) {
     float a = x, b = x;
     asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
-    return fmaxf(a, b);
+    return max3f(a, b, b);
 }
 
-// v_max3_f32 without the canonicalizing moves the compiler adds in front of
-// fmaxf when it cannot prove its inputs canonical (no NaN reaches this kernel).
-__device__ inline float max3f(float a, float b, float c) {
-    float r;
-    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-    return r;
-}
 
 // S += A B^T with the accumulators in architectural VGPRs. At one wave per SIMD the compiler
 // gives every MFMA of a kernel the accumulator-register form; where O already fills the 256
@@ -275,8 +276,8 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
     auto stage_piece = [&](W64KTile &kb, W64VTile &vb, int j, const uint32_t (&x)[4]) __attribute__((always_inline)) {
         if constexpr (kInt8) {
             uint4 h;
-            i8x4_to_f16(x[0], h.x, h.y);
-            i8x4_to_f16(x[1], h.z, h.w);
+            i8x4_to_f16_sdwa(x[0], h.x, h.y);
+            i8x4_to_f16_sdwa(x[1], h.z, h.w);
             if (j < 4)
                 *reinterpret_cast<uint4 *>(kb.k + (krow0 + 4 * (j >> 1)) * kKStride + kchunk * 16 + 8 * (j & 1)) = h;
             else
@@ -504,7 +505,7 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
                 mpart[rb][0] = max3f(max3f(t[0], t[1], t[2]), max3f(t[3], t[4], t[5]), max3f(t[6], t[7], t[8]));
                 mpart[rb][1] = max3f(max3f(t[9], t[10], t[11]), max3f(t[12], t[13], t[14]), t[15]);
             } else if (j == 9) {
-                ymax[rb] = pair_max(fmaxf(mpart[rb][0], mpart[rb][1]));
+                ymax[rb] = pair_max(max3f(mpart[rb][0], mpart[rb][1], mpart[rb][1]));
                 need[rb] = (ymax[rb] > 8.0f) | ((m[rb] == -INFINITY) & (ymax[rb] > -INFINITY));   // no branch
             }
         };

@@ -27,6 +27,18 @@ __device__ inline void i8x4_to_f16(uint32_t w, uint32_t &lo, uint32_t &hi) {
     hi = __builtin_bit_cast(uint32_t, hb);
 }
 
+// The same conversion in four instructions: each converts one byte, sign-extended by the
+// operand select (SDWA), from INT16 to FP16 and writes one half of its destination, the
+// second keeping the half the first wrote. Exact: every INT8 value is an FP16 integer.
+__device__ inline void i8x4_to_f16_sdwa(uint32_t w, uint32_t &lo, uint32_t &hi) {
+    asm("v_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+        "v_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1\n\t"
+        "v_cvt_f16_i16_sdwa %1, sext(%2) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_2\n\t"
+        "v_cvt_f16_i16_sdwa %1, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_3"
+        : "=&v"(lo), "=&v"(hi)
+        : "v"(w));
+}
+
 // Eight INT8 codes (two dwords) -> half8 operand, in byte order.
 __device__ inline half8 i8x8_to_half8(uint32_t w0, uint32_t w1) {
     uint32_t r[4];
