@@ -223,15 +223,16 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
     auto load_raw = [&](uint32_t key0) __attribute__((always_inline)) {
         Raw r;
         key0 = min(key0, last_key0);
+        // (byte offsets below 2^28 for the 262144-token window: 32-bit offsets from the bases)
         if constexpr (kInt8) {
             const int8_t *kcodes = (const int8_t *)p.k, *vcodes = (const int8_t *)p.v;
             const uint32_t ka = min(key0 + (uint32_t)krow0, p.keys - 1), kb2 = min(key0 + (uint32_t)krow0 + 4, p.keys - 1);
-            r.w[0] = *reinterpret_cast<const uint4 *>(kcodes + (size_t)((ka * 2 + g) * 256 + kchunk * 16));
-            r.w[1] = *reinterpret_cast<const uint4 *>(kcodes + (size_t)((kb2 * 2 + g) * 256 + kchunk * 16));
-            const size_t offv = (size_t)value_index((uint64_t)key0 * 2 + g, 0) + (size_t)tid * 256;
+            r.w[0] = *reinterpret_cast<const uint4 *>(kcodes + ((ka * 2 + g) * 256 + kchunk * 16));
+            r.w[1] = *reinterpret_cast<const uint4 *>(kcodes + ((kb2 * 2 + g) * 256 + kchunk * 16));
+            const uint32_t offv = (uint32_t)value_index((uint64_t)key0 * 2 + g, 0) + (uint32_t)tid * 256;
             r.w[2] = *reinterpret_cast<const uint4 *>(vcodes + offv);
-            r.w[3] = *reinterpret_cast<const uint4 *>(vcodes + offv + 16);
-            const size_t at = (size_t)min(key0 + (uint32_t)(tid & 31), p.keys - 1) * 2 + g;
+            r.w[3] = *reinterpret_cast<const uint4 *>(vcodes + (offv + 16));
+            const uint32_t at = min(key0 + (uint32_t)(tid & 31), p.keys - 1) * 2 + g;
             r.ks = p.ks[at];
             r.vs = p.vs[at];
         } else {
@@ -240,8 +241,8 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const uint32_t key = min(key0 + (uint32_t)(4 * fgroup + j), p.keys - 1);
-                r.w[j] = *reinterpret_cast<const uint4 *>(kh + ((size_t)key * 2 + g) * 256 + 8 * fpiece);
-                r.w[4 + j] = *reinterpret_cast<const uint4 *>(vh + ((size_t)key * 2 + g) * 256 + 8 * fpiece);
+                r.w[j] = *reinterpret_cast<const uint4 *>(kh + ((key * 2 + g) * 256 + 8 * fpiece));
+                r.w[4 + j] = *reinterpret_cast<const uint4 *>(vh + ((key * 2 + g) * 256 + 8 * fpiece));
             }
             r.ks = r.vs = 0.0f;
         }
@@ -386,11 +387,10 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
     };
 
     // The softmax of tile n - 1, finished in phase A of tile n: element v of row block rb of
-    // exp2(S) with S scaled and shifted by the running maximum, times the key's V scale / vs_ref
-    // into P (FP16, RNE), and into the row's sum.
-    auto exp_elem = [&](int rb, int v, const floatx16 (&sp)[2], const float4 (&v4)[4], half8 (&pn)[2][2],
-                        float (&lsum)[2]) __attribute__((always_inline)) {
-        const float e = __builtin_amdgcn_exp2f(sp[rb][v]);
+    // exp2(S) (e, with S scaled and shifted by the running maximum), times the key's V scale /
+    // vs_ref into P (FP16, RNE), and into the row's sum.
+    auto exp_elem = [&](int rb, int v, float e, const float4 (&v4)[4], half8 (&pn)[2][2], float (&lsum)[2])
+        __attribute__((always_inline)) {
         const float4 &w = v4[v >> 2];
         const float vsc = (v & 3) == 0 ? w.x : (v & 3) == 1 ? w.y : (v & 3) == 2 ? w.z : w.w;
         pn[rb][v >> 3][v & 7] = (_Float16)(e * vsc);
@@ -406,6 +406,15 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
         float4 v4[4];
         load_scales(n - 1, true, v4);
         float lsum[2] = {0.0f, 0.0f};
+        // INT8: exp2 runs one step ahead of its use: the wave issues in order, and a product
+        // right behind its exponential would stall for the transcendental's latency (FP16 KV:
+        // in place, its larger staging registers leave no room for the two in flight)
+        constexpr bool kAhead = kInt8;
+        float ex[2] = {0.0f, 0.0f};
+        if constexpr (kAhead) {
+            ex[0] = __builtin_amdgcn_exp2f(sp[0][0]);
+            ex[1] = __builtin_amdgcn_exp2f(sp[1][0]);
+        }
         {
             const _Float16 *kr = kbuf[n & 1].k + qk_key_row(i) * kKStride + 8 * kk;
             half8 kop[4];                                       // K operands, read three steps ahead
@@ -433,12 +442,20 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
                 else
                     s_mfma(sc[0], kop[c & 3], q0);
                 {
-                    // this step's inputs follow the MFMA, the previous step's row sum precedes it
-                    float z = sp[0][c];
+                    // the input of the step's exponential follows the MFMA, the previous step's row
+                    // sum precedes it
+                    const int cz = kAhead ? (c < 15 ? c + 1 : 15) : c;
+                    float z = sp[0][cz];
                     after_mfma(z, lsum[1]);
-                    sp[0][c] = z;
+                    sp[0][cz] = z;
                 }
-                exp_elem(0, c, sp, v4, pn, lsum);
+                if constexpr (kAhead) {
+                    const float e = ex[0];
+                    if (c < 15) ex[0] = __builtin_amdgcn_exp2f(sp[0][c + 1]);
+                    exp_elem(0, c, e, v4, pn, lsum);
+                } else {
+                    exp_elem(0, c, __builtin_amdgcn_exp2f(sp[0][c]), v4, pn, lsum);
+                }
                 if (c == 0)
                     s_mfma_first(sc[1], kop[c & 3], q1);
                 else if (c < 15)
@@ -446,11 +463,18 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
                 else
                     s_mfma_last(sc[1], kop[c & 3], q1);
                 {
-                    float z = sp[1][c];
+                    const int cz = kAhead ? (c < 15 ? c + 1 : 15) : c;
+                    float z = sp[1][cz];
                     after_mfma(z, lsum[0]);
-                    sp[1][c] = z;
+                    sp[1][cz] = z;
                 }
-                exp_elem(1, c, sp, v4, pn, lsum);
+                if constexpr (kAhead) {
+                    const float e = ex[1];
+                    if (c < 15) ex[1] = __builtin_amdgcn_exp2f(sp[1][c + 1]);
+                    exp_elem(1, c, e, v4, pn, lsum);
+                } else {
+                    exp_elem(1, c, __builtin_amdgcn_exp2f(sp[1][c]), v4, pn, lsum);
+                }
             }
         }
 #pragma unroll
