@@ -397,14 +397,43 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
         lsum[rb] += e;
     };
 
+    // The first LDS reads of each phase are issued one phase early (prefetch_a at the end of phase
+    // B, prefetch_b before the barrier), so that their latency overlaps the previous phase's tail
+    // and the barrier. Both read buffers no phase writes until after the next barrier: K(n) was
+    // staged in phase B of tile n - 2, V(n - 1) and the scales of tiles n - 1 and n earlier still.
+    // (INT8 only: the FP16 staging keeps more registers live, and the early reads then spill)
+    constexpr bool kEarly = kInt8;
+    static_assert(kW64QRegs >= 3, "the first three QK steps take their Q^T chunks from registers");
+    auto prefetch_a = [&](int n, float4 (&v4)[4], half8 (&kop)[3]) __attribute__((always_inline)) {
+        load_scales(n - 1, true, v4);
+        const _Float16 *kr = kbuf[n & 1].k + qk_key_row(i) * kKStride + 8 * kk;
+#pragma unroll
+        for (int c = 0; c < 3; c++) kop[c] = *reinterpret_cast<const half8 *>(kr + 16 * c);
+    };
+    const int vsw = (i >> 2) & 3;   // V^T rows 32dt + i share the swizzle of row i
+    // V(n - 1)^T operand of PV step j (16-key step j / 8, dimension tile j % 8)
+    auto vop = [&](int n, int j) __attribute__((always_inline)) {
+        const _Float16 *vt = vbuf[(n + kW64VBufs - 1) % kW64VBufs].v + i * kW64Keys;
+        return *reinterpret_cast<const half8 *>(vt + 32 * (j & 7) * kW64Keys + 8 * ((2 * (j >> 3) + kk) ^ vsw));
+    };
+    auto prefetch_b = [&](int n, float4 (&k4)[4], half8 (&vr)[kW64VAhead]) __attribute__((always_inline)) {
+        load_scales(n, false, k4);
+#pragma unroll
+        for (int j = 0; j < kW64VAhead; j++) vr[j] = vop(n, j);
+    };
+
     // Phase A of tile n: S(n) for both row blocks (K operands read three steps ahead) and the
     // exponentials of tile n - 1 (P(n - 1) and l), spread between the MFMAs. One path for every
     // n: after the last tile (n = ntiles) the MFMAs multiply the finite codes staged for keys past
-    // the split, an S that phase B replaces with -inf.
-    auto phase_a = [&](int n, floatx16 (&sc)[2], floatx16 (&sp)[2], const float (&dec)[2], half8 (&pn)[2][2])
-        __attribute__((always_inline)) {
-        float4 v4[4];
-        load_scales(n - 1, true, v4);
+    // the split, an S that phase B replaces with -inf. v4 (the V scales of tile n - 1) and the
+    // first three K operands come from prefetch_a.
+    auto phase_a = [&](int n, floatx16 (&sc)[2], floatx16 (&sp)[2], const float (&dec)[2], half8 (&pn)[2][2],
+                       const float4 (&v4pre)[4], const half8 (&kpre_in)[3]) __attribute__((always_inline)) {
+        float4 v4own[4];
+        half8 kown[3];
+        if constexpr (!kEarly) prefetch_a(n, v4own, kown);
+        const float4 (&v4)[4] = kEarly ? v4pre : v4own;
+        const half8 (&kpre)[3] = kEarly ? kpre_in : kown;
         float lsum[2] = {0.0f, 0.0f};
         // INT8: exp2 runs one step ahead of its use: the wave issues in order, and a product
         // right behind its exponential would stall for the transcendental's latency (FP16 KV:
@@ -420,12 +449,7 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
             half8 kop[4];                                       // K operands, read three steps ahead
             half8 qop_l[4][2];                                  // Q^T chunks from LDS, likewise
 #pragma unroll
-            for (int c = 0; c < 3; c++) {
-                kop[c] = *reinterpret_cast<const half8 *>(kr + 16 * c);
-                if (c >= kW64QRegs)
-#pragma unroll
-                    for (int rb = 0; rb < 2; rb++) qop_l[c & 3][rb] = qop_at(rb, c);
-            }
+            for (int c = 0; c < 3; c++) kop[c] = kpre[c];
 #pragma unroll
             for (int c = 0; c < 16; c++) {
                 if (c + 3 < 16) {
@@ -499,21 +523,19 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
     // accumulators must not meet branches): before the first tile P is zero and the V buffer it
     // reads is zero-filled; after the last (past), S is -inf, which leaves m, l and P unchanged.
     auto phase_b = [&](int n, floatx16 (&sc)[2], const half8 (&pp)[2][2], bool (&need)[2], float (&ymax)[2], bool past,
-                       Raw &raw) __attribute__((always_inline)) {
+                       Raw &raw, const float4 (&k4pre)[4], const half8 (&vpre_in)[kW64VAhead]) __attribute__((always_inline)) {
+        float4 k4own[4];
+        half8 vown[kW64VAhead];
+        if constexpr (!kEarly) prefetch_b(n, k4own, vown);
+        const float4 (&k4)[4] = kEarly ? k4pre : k4own;
+        const half8 (&vpre)[kW64VAhead] = kEarly ? vpre_in : vown;
         const uint32_t key2 = kbeg + (uint32_t)(n + 2) * kW64Keys;
         W64KTile &kdst = kbuf[n & 1];                 // tile n's, read in phase A of tile n
         W64VTile &vdst = vbuf[(n + 2) % kW64VBufs];   // tile n - 2's, read in phase B of tile n - 1
-        float4 k4[4];
-        load_scales(n, false, k4);
         float add[2];
 #pragma unroll
         for (int rb = 0; rb < 2; rb++)   // past the last tile: -inf for every key, whatever the (finite) S and K scales
             add[rb] = past ? -INFINITY : -(m[rb] == -INFINITY ? 0.0f : m[rb]);
-        const _Float16 *vt = vbuf[(n + kW64VBufs - 1) % kW64VBufs].v + i * kW64Keys;
-        const int vsw = (i >> 2) & 3;   // rows 32dt + i share the swizzle of row i
-        auto vop = [&](int j) __attribute__((always_inline)) {   // step j: 16-key step u = j / 8, d tile dt = j % 8
-            return *reinterpret_cast<const half8 *>(vt + 32 * (j & 7) * kW64Keys + 8 * ((2 * (j >> 3) + kk) ^ vsw));
-        };
         // step j < 8 scales elements 2j, 2j + 1 of each row block; steps 8-9 take the maxima
         auto scale_pair = [&](int rb, int j) __attribute__((always_inline)) {
             float x = sc[rb][2 * j], y = sc[rb][2 * j + 1];
@@ -535,10 +557,10 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
         };
         half8 vring[kW64VAhead + 1];
 #pragma unroll
-        for (int j = 0; j < kW64VAhead; j++) vring[j] = vop(j);
+        for (int j = 0; j < kW64VAhead; j++) vring[j] = vpre[j];
 #pragma unroll
         for (int j = 0; j < 16; j++) {
-            if (j + kW64VAhead < 16) vring[(j + kW64VAhead) % (kW64VAhead + 1)] = vop(j + kW64VAhead);
+            if (j + kW64VAhead < 16) vring[(j + kW64VAhead) % (kW64VAhead + 1)] = vop(n, j + kW64VAhead);
             const half8 va = vring[j % (kW64VAhead + 1)];
             o_mfma(o[0][j & 7], va, pp[0][j >> 3]);
             if (j < 8) scale_pair(0, j);
@@ -621,6 +643,9 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
     for (int rb = 0; rb < 2; rb++)
 #pragma unroll
         for (int v = 0; v < 16; v++) sp[rb][v] = -INFINITY;
+    float4 v4n[4];
+    half8 kopn[3];
+    if constexpr (kEarly) prefetch_a(0, v4n, kopn);
     for (int n = 0; n <= ntiles; n++) {
         // the accumulators live in the accumulator registers across iterations
 #pragma unroll
@@ -628,11 +653,25 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
 #pragma unroll
             for (int dt = 0; dt < 8; dt++) asm volatile("" : "+a"(o[rb][dt]));
         floatx16 sc[2];
-        phase_a(n, sc, sp, dec, pb);
-        __syncthreads();
+        phase_a(n, sc, sp, dec, pb, v4n, kopn);
+        // The barrier between the phases, with phase B's first reads in flight across it: this
+        // wave's LDS writes (the staging of phase B of tile n - 1) and phase A's reads are complete
+        // first, as a work-group barrier's release would have them, and the assembly barrier keeps
+        // the compiler from waiting for the reads issued after that.
+        float4 k4[4];
+        half8 vpre[kW64VAhead];
+        if constexpr (kEarly) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            prefetch_b(n, k4, vpre);
+            asm volatile("s_barrier" ::: "memory");
+        } else {
+            __syncthreads();
+        }
         bool need[2];
         float ymax[2];
-        phase_b(n, sc, pb, need, ymax, n == ntiles, raw);
+        phase_b(n, sc, pb, need, ymax, n == ntiles, raw, k4, vpre);
+        // after the last tile: unused reads of buffers in range
+        if constexpr (kEarly) prefetch_a(n + 1, v4n, kopn);
         dec[0] = dec[1] = 1.0f;
         const bool masked = kbeg + (uint32_t)n * kW64Keys + kW64Keys - 1 > wave_min_limit;
         if (masked | (__ballot(need[0] | need[1]) != 0)) {   // bitwise: both sides computed
