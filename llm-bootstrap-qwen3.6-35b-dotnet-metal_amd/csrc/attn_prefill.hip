@@ -123,6 +123,12 @@ __device__ __forceinline__ void after_mfma(uint32_t &x, uint32_t &y) { asm volat
 __device__ __forceinline__ void after_mfma(uint32_t &x, uint32_t &y, uint32_t &z, uint32_t &w) {
     asm volatile("" : "+v"(x), "+v"(y), "+v"(z), "+v"(w));
 }
+// The other side: values named here are computed before the next assembly MFMA (volatile
+// assembly keeps its order), so that a step's vector work stays between its two MFMAs instead of
+// collecting in long runs the matrix pipe waits through.
+__device__ __forceinline__ void before_mfma(float x, float y) { asm volatile("" ::"v"(x), "v"(y)); }
+__device__ __forceinline__ void before_mfma(float x, float y, uint32_t z) { asm volatile("" ::"v"(x), "v"(y), "v"(z)); }
+__device__ __forceinline__ void before_mfma(uint32_t x, uint32_t y) { asm volatile("" ::"v"(x), "v"(y)); }
 
 // ---------------------------------------------------------------- prefill, one wave per SIMD
 //
@@ -138,13 +144,17 @@ __device__ __forceinline__ void after_mfma(uint32_t &x, uint32_t &y, uint32_t &z
 //   B: O += V(n - 1)^T P(n - 1) (32 MFMAs), interleaved with S(n)'s scaling and row maxima, the
 //      staging of tile n + 2 (INT8: codes converted to FP16; FP16: copied, V transposed) and
 //      the loads of tile n + 3.
-// Rows whose maximum grows by more than 2^8, and tiles on the causal diagonal, take a fix-up
+// Rows whose maximum grows by more than 2^15, and tiles on the causal diagonal, take a fix-up
 // after phase B (the general softmax); the common case needs no maximum before exp2. The
 // MFMAs are inline assembly, so that their order, and the operand reads placed three steps
 // ahead of them, are kept; each step's vector work is tied behind its MFMA. K tiles are
 // double-buffered and V tiles (with the tile's scales) quadruple-buffered: every buffer a
 // phase writes was last read before the previous barrier.
 constexpr int kW64Keys = 32;               // keys per tile
+// Lazy running maximum: a row rebases when a tile's maximum exceeds it by more than 2^kRebase
+// (log2 units). Exponentials then stay <= 2^15 = 32768, so P = e * vs / vs_ref (<= e) is finite in
+// FP16 (largest 65504); a maximum that lags only makes the kept exponentials larger.
+constexpr float kRebase = 15.0f;
 constexpr int kW64VBufs = 4;               // V^T tiles in LDS
 #ifndef BOOT_W64_QLDS
 #define BOOT_W64_QLDS 7
@@ -220,32 +230,50 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
         uint4 w[8];    // INT8: K rows krow0, krow0 + 4, V page row t; FP16: 4 K pieces, 4 V keys
         float ks, vs;  // INT8: scales of key t % 32
     };
-    auto load_raw = [&](uint32_t key0) __attribute__((always_inline)) {
-        Raw r;
-        key0 = min(key0, last_key0);
+    // A tile's loads in three parts, so that phase B can reissue each as soon as the staging has
+    // consumed its registers: the scales, the K codes (pieces 0-3), the V codes (pieces 4-7).
+    // (key0: the tile's first key, at most last_key0)
+    auto load_part = [&](Raw &r, uint32_t key0, int part) __attribute__((always_inline)) {
         // (byte offsets below 2^28 for the 262144-token window: 32-bit offsets from the bases)
         if constexpr (kInt8) {
-            const int8_t *kcodes = (const int8_t *)p.k, *vcodes = (const int8_t *)p.v;
-            const uint32_t ka = min(key0 + (uint32_t)krow0, p.keys - 1), kb2 = min(key0 + (uint32_t)krow0 + 4, p.keys - 1);
-            r.w[0] = *reinterpret_cast<const uint4 *>(kcodes + ((ka * 2 + g) * 256 + kchunk * 16));
-            r.w[1] = *reinterpret_cast<const uint4 *>(kcodes + ((kb2 * 2 + g) * 256 + kchunk * 16));
-            const uint32_t offv = (uint32_t)value_index((uint64_t)key0 * 2 + g, 0) + (uint32_t)tid * 256;
-            r.w[2] = *reinterpret_cast<const uint4 *>(vcodes + offv);
-            r.w[3] = *reinterpret_cast<const uint4 *>(vcodes + (offv + 16));
-            const uint32_t at = min(key0 + (uint32_t)(tid & 31), p.keys - 1) * 2 + g;
-            r.ks = p.ks[at];
-            r.vs = p.vs[at];
+            if (part == 0) {
+                const uint32_t at = (min(key0 + (uint32_t)(tid & 31), p.keys - 1) * 2 + g) * 4;   // bytes
+                r.ks = *reinterpret_cast<const float *>(reinterpret_cast<const char *>(p.ks) + at);
+                r.vs = *reinterpret_cast<const float *>(reinterpret_cast<const char *>(p.vs) + at);
+            } else if (part == 1) {
+                const int8_t *kcodes = (const int8_t *)p.k;
+                const uint32_t ka = min(key0 + (uint32_t)krow0, p.keys - 1), kb2 = min(key0 + (uint32_t)krow0 + 4, p.keys - 1);
+                r.w[0] = *reinterpret_cast<const uint4 *>(kcodes + ((ka * 2 + g) * 256 + kchunk * 16));
+                r.w[1] = *reinterpret_cast<const uint4 *>(kcodes + ((kb2 * 2 + g) * 256 + kchunk * 16));
+            } else {
+                const int8_t *vcodes = (const int8_t *)p.v;
+                const uint32_t offv = (uint32_t)value_index((uint64_t)key0 * 2 + g, 0) + (uint32_t)tid * 256;
+                r.w[2] = *reinterpret_cast<const uint4 *>(vcodes + offv);
+                r.w[3] = *reinterpret_cast<const uint4 *>(vcodes + (offv + 16));
+            }
         } else {
             // keys past K are clamped to K - 1: the cache beyond K (NaN padding) is never read
             const _Float16 *kh = (const _Float16 *)p.k, *vh = (const _Float16 *)p.v;
+            if (part == 0) {
+                r.ks = r.vs = 0.0f;
+            } else {
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t key = min(key0 + (uint32_t)(4 * fgroup + j), p.keys - 1);
-                r.w[j] = *reinterpret_cast<const uint4 *>(kh + ((key * 2 + g) * 256 + 8 * fpiece));
-                r.w[4 + j] = *reinterpret_cast<const uint4 *>(vh + ((key * 2 + g) * 256 + 8 * fpiece));
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t key = min(key0 + (uint32_t)(4 * fgroup + j), p.keys - 1);
+                    if (part == 1)
+                        r.w[j] = *reinterpret_cast<const uint4 *>(kh + ((key * 2 + g) * 256 + 8 * fpiece));
+                    else
+                        r.w[4 + j] = *reinterpret_cast<const uint4 *>(vh + ((key * 2 + g) * 256 + 8 * fpiece));
+                }
             }
-            r.ks = r.vs = 0.0f;
         }
+    };
+    auto load_raw = [&](uint32_t key0) __attribute__((always_inline)) {
+        Raw r;   // (the order phase B issues them in: the waits in the loop count on it)
+        key0 = min(key0, last_key0);
+        load_part(r, key0, 0);
+        load_part(r, key0, 1);
+        load_part(r, key0, 2);
         return r;
     };
     float vs_inv = 0.0f;
@@ -274,15 +302,19 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
             }
         }
     };
+    // INT8 piece j (8 converted codes): K rows for j < 4, V^T row t for j >= 4
+    auto store_piece = [&](W64KTile &kb, W64VTile &vb, int j, const uint4 &h) __attribute__((always_inline)) {
+        if (j < 4)
+            *reinterpret_cast<uint4 *>(kb.k + (krow0 + 4 * (j >> 1)) * kKStride + kchunk * 16 + 8 * (j & 1)) = h;
+        else
+            *reinterpret_cast<uint4 *>(vb.v + tid * kW64Keys + 8 * ((j - 4) ^ vsw_stage)) = h;
+    };
     auto stage_piece = [&](W64KTile &kb, W64VTile &vb, int j, const uint32_t (&x)[4]) __attribute__((always_inline)) {
         if constexpr (kInt8) {
             uint4 h;
             i8x4_to_f16_sdwa(x[0], h.x, h.y);
             i8x4_to_f16_sdwa(x[1], h.z, h.w);
-            if (j < 4)
-                *reinterpret_cast<uint4 *>(kb.k + (krow0 + 4 * (j >> 1)) * kKStride + kchunk * 16 + 8 * (j & 1)) = h;
-            else
-                *reinterpret_cast<uint4 *>(vb.v + tid * kW64Keys + 8 * ((j - 4) ^ vsw_stage)) = h;
+            store_piece(kb, vb, j, h);
         } else if (j < 4) {
             *reinterpret_cast<uint4 *>(kb.k + (4 * fgroup + j) * kKStride + 8 * fpiece) = make_uint4(x[0], x[1], x[2], x[3]);
         } else {
@@ -299,8 +331,10 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
         const int t = tid & 31;
         const bool inside = key0 + t < p.keys;   // poisoned tails beyond K never reach S or P
         if constexpr (kInt8) {
-            vb.ks[t] = inside ? r.ks * (kLog2e / 16.0f) : 0.0f;
-            vb.vs[t] = inside ? r.vs * vs_inv : 0.0f;
+            float ks = r.ks, vs = r.vs;
+            after_mfma(ks, vs);   // the products stay where the call is (not hoisted to the loads)
+            vb.ks[t] = inside ? ks * (kLog2e / 16.0f) : 0.0f;
+            vb.vs[t] = inside ? vs * vs_inv : 0.0f;
         } else {
             vb.ks[t] = inside ? kLog2e / 16.0f : 0.0f;
             vb.vs[t] = inside ? 1.0f : 0.0f;
@@ -349,6 +383,12 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
         float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, vs_ref > 0.0f ? 1.0f / vs_ref : 0.0f)));
     stage(kbuf[0], vbuf[0], kbeg, raw0);
     stage(kbuf[1], vbuf[1], kbeg + kW64Keys, raw1);
+    // the query chunks are in their registers before the loop (a use here makes the compiler wait
+    // for their loads once, instead of before their MFMAs on every tile)
+#pragma unroll
+    for (int rb = 0; rb < 2; rb++)
+#pragma unroll
+        for (int c = 0; c < kW64QRegs; c++) asm volatile("" ::"v"(qop[rb][c]));
     Raw raw = load_raw(kbeg + 2 * kW64Keys);   // staged in phase B of tile 0
     {
         // "tile -1", whose zero probabilities the first PV multiplies: zero V^T codes and scales,
@@ -367,6 +407,7 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
 #pragma unroll
             for (int v = 0; v < 16; v++) o[rb][dt][v] = 0.0f;
     float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
+    float thr[2] = {-INFINITY, -INFINITY};   // a row needs the general softmax when its tile maximum exceeds thr
     half8 pb[2][2];          // P(n - 1): [row block][16-key step]
 #pragma unroll
     for (int rb = 0; rb < 2; rb++)
@@ -377,24 +418,53 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
                              : __builtin_bit_cast(half8, qlds[c < kW64QRegs ? 0 : c - kW64QRegs][rb][tid]);
     };
 
-    // the K (or V) scales of tile n's keys (n >= -1), as the softmax lanes hold them
-    auto load_scales = [&](int n, bool v, float4 (&x4)[4]) __attribute__((always_inline)) {
-        const W64VTile &sb = vbuf[(n + kW64VBufs) % kW64VBufs];
+    // The loop addresses its buffers by byte offsets that rotate from tile to tile (K: tile n's at
+    // kcur; V: tiles n - 1, n, n + 1, n + 2 at vm1, vc0, vc1, vc2), not by index arithmetic per tile.
+    auto ktile = [&](uint32_t off) __attribute__((always_inline)) -> W64KTile & {
+        return *reinterpret_cast<W64KTile *>(reinterpret_cast<unsigned char *>(kbuf) + off);
+    };
+    auto vtile = [&](uint32_t off) __attribute__((always_inline)) -> W64VTile & {
+        return *reinterpret_cast<W64VTile *>(reinterpret_cast<unsigned char *>(vbuf) + off);
+    };
+    constexpr uint32_t kKT = sizeof(W64KTile), kVT = sizeof(W64VTile);
+    uint32_t kcur = 0, vm1 = (kW64VBufs - 1) * kVT, vc0 = 0, vc1 = kVT, vc2 = 2 * kVT;   // tile 0
+
+    // the K (or V) scales of a tile's keys, as the softmax lanes hold them
+    auto load_scales = [&](uint32_t vo, bool v, float4 (&x4)[4]) __attribute__((always_inline)) {
+        const W64VTile &sb = vtile(vo);
         const float *src = v ? sb.vs : sb.ks;
 #pragma unroll
         for (int q4 = 0; q4 < 4; q4++)
             x4[q4] = *reinterpret_cast<const float4 *>(src + 16 * (q4 >> 1) + 8 * kk + 4 * (q4 & 1));
     };
 
+    auto load_scale4 = [&](uint32_t vo, bool v, int q4) __attribute__((always_inline)) {
+        const W64VTile &sb = vtile(vo);
+        const float *src = v ? sb.vs : sb.ks;
+        return *reinterpret_cast<const float4 *>(src + 16 * (q4 >> 1) + 8 * kk + 4 * (q4 & 1));
+    };
+
     // The softmax of tile n - 1, finished in phase A of tile n: element v of row block rb of
     // exp2(S) (e, with S scaled and shifted by the running maximum), times the key's V scale /
     // vs_ref into P (FP16, RNE), and into the row's sum.
-    auto exp_elem = [&](int rb, int v, float e, const float4 (&v4)[4], half8 (&pn)[2][2], float (&lsum)[2])
-        __attribute__((always_inline)) {
-        const float4 &w = v4[v >> 2];
+    // Elements are packed in pairs as the odd one completes (the product of the even one waits in
+    // `prv`), and the pair goes to its P register at once.
+    typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+    auto exp_elem = [&](int rb, int v, float e, const float4 &w, uint32_t (&pw)[2][8], float (&lsum)[2],
+                        float (&prv)[2]) __attribute__((always_inline)) {
         const float vsc = (v & 3) == 0 ? w.x : (v & 3) == 1 ? w.y : (v & 3) == 2 ? w.z : w.w;
-        pn[rb][v >> 3][v & 7] = (_Float16)(e * vsc);
+        const float prod = e * vsc;
         lsum[rb] += e;
+        uint32_t d;
+        if (v & 1) {
+            const half2_t h = {(_Float16)prv[rb], (_Float16)prod};
+            d = __builtin_bit_cast(uint32_t, h);
+            pw[rb][v >> 1] = d;
+        } else {
+            prv[rb] = prod;
+            d = __builtin_bit_cast(uint32_t, prod);
+        }
+        return d;
     };
 
     // The first LDS reads of each phase are issued one phase early (prefetch_a at the end of phase
@@ -404,22 +474,23 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
     // (INT8 only: the FP16 staging keeps more registers live, and the early reads then spill)
     constexpr bool kEarly = kInt8;
     static_assert(kW64QRegs >= 3, "the first three QK steps take their Q^T chunks from registers");
-    auto prefetch_a = [&](int n, float4 (&v4)[4], half8 (&kop)[3]) __attribute__((always_inline)) {
-        load_scales(n - 1, true, v4);
-        const _Float16 *kr = kbuf[n & 1].k + qk_key_row(i) * kKStride + 8 * kk;
+    // (ko, vo: the K tile phase A reads and the V tile whose scales its products take)
+    auto prefetch_a = [&](uint32_t ko, uint32_t vo, float4 &v0, half8 (&kop)[3]) __attribute__((always_inline)) {
+        v0 = load_scale4(vo, true, 0);
+        const _Float16 *kr = ktile(ko).k + qk_key_row(i) * kKStride + 8 * kk;
 #pragma unroll
         for (int c = 0; c < 3; c++) kop[c] = *reinterpret_cast<const half8 *>(kr + 16 * c);
     };
     const int vsw = (i >> 2) & 3;   // V^T rows 32dt + i share the swizzle of row i
     // V(n - 1)^T operand of PV step j (16-key step j / 8, dimension tile j % 8)
-    auto vop = [&](int n, int j) __attribute__((always_inline)) {
-        const _Float16 *vt = vbuf[(n + kW64VBufs - 1) % kW64VBufs].v + i * kW64Keys;
+    auto vop = [&](int j) __attribute__((always_inline)) {
+        const _Float16 *vt = vtile(vm1).v + i * kW64Keys;
         return *reinterpret_cast<const half8 *>(vt + 32 * (j & 7) * kW64Keys + 8 * ((2 * (j >> 3) + kk) ^ vsw));
     };
-    auto prefetch_b = [&](int n, float4 (&k4)[4], half8 (&vr)[kW64VAhead]) __attribute__((always_inline)) {
-        load_scales(n, false, k4);
+    auto prefetch_b = [&](float4 (&k4)[4], half8 (&vr)[kW64VAhead]) __attribute__((always_inline)) {
+        load_scales(vc0, false, k4);
 #pragma unroll
-        for (int j = 0; j < kW64VAhead; j++) vr[j] = vop(n, j);
+        for (int j = 0; j < kW64VAhead; j++) vr[j] = vop(j);
     };
 
     // Phase A of tile n: S(n) for both row blocks (K operands read three steps ahead) and the
@@ -428,81 +499,78 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
     // the split, an S that phase B replaces with -inf. v4 (the V scales of tile n - 1) and the
     // first three K operands come from prefetch_a.
     auto phase_a = [&](int n, floatx16 (&sc)[2], floatx16 (&sp)[2], const float (&dec)[2], half8 (&pn)[2][2],
-                       const float4 (&v4pre)[4], const half8 (&kpre_in)[3]) __attribute__((always_inline)) {
-        float4 v4own[4];
+                       const float4 &v0pre, const half8 (&kpre_in)[3]) __attribute__((always_inline)) {
+        float4 v0own;
         half8 kown[3];
-        if constexpr (!kEarly) prefetch_a(n, v4own, kown);
-        const float4 (&v4)[4] = kEarly ? v4pre : v4own;
+        if constexpr (!kEarly) prefetch_a(kcur, vm1, v0own, kown);
+        // the V scales of tile n - 1, four keys per read, each read four steps before its use
+        float4 vq[2];
+        vq[0] = kEarly ? v0pre : v0own;
         const half8 (&kpre)[3] = kEarly ? kpre_in : kown;
         float lsum[2] = {0.0f, 0.0f};
         // INT8: exp2 runs one step ahead of its use: the wave issues in order, and a product
         // right behind its exponential would stall for the transcendental's latency (FP16 KV:
         // in place, its larger staging registers leave no room for the two in flight)
         constexpr bool kAhead = kInt8;
-        float ex[2] = {0.0f, 0.0f};
+        float ex[2] = {0.0f, 0.0f}, prv[2] = {0.0f, 0.0f};
+        // P(n - 1) as it is packed, in fresh registers (inserting into the previous tile's P would
+        // keep its registers live into this phase)
+        uint32_t pw[2][8];
         if constexpr (kAhead) {
             ex[0] = __builtin_amdgcn_exp2f(sp[0][0]);
             ex[1] = __builtin_amdgcn_exp2f(sp[1][0]);
         }
         {
-            const _Float16 *kr = kbuf[n & 1].k + qk_key_row(i) * kKStride + 8 * kk;
+            const _Float16 *kr = ktile(kcur).k + qk_key_row(i) * kKStride + 8 * kk;
             half8 kop[4];                                       // K operands, read three steps ahead
-            half8 qop_l[4][2];                                  // Q^T chunks from LDS, likewise
+            half8 qop_l[3][2];                                  // Q^T chunks from LDS, two steps ahead
 #pragma unroll
             for (int c = 0; c < 3; c++) kop[c] = kpre[c];
 #pragma unroll
             for (int c = 0; c < 16; c++) {
-                if (c + 3 < 16) {
-                    kop[(c + 3) & 3] = *reinterpret_cast<const half8 *>(kr + 16 * (c + 3));
-                    if (c + 3 >= kW64QRegs)
+                if (c + 3 < 16) kop[(c + 3) & 3] = *reinterpret_cast<const half8 *>(kr + 16 * (c + 3));
+                if ((c & 3) == 0 && c < 12) vq[((c >> 2) + 1) & 1] = load_scale4(vm1, true, (c >> 2) + 1);
+                if (c + 2 < 16 && c + 2 >= kW64QRegs)
 #pragma unroll
-                        for (int rb = 0; rb < 2; rb++) qop_l[(c + 3) & 3][rb] = qop_at(rb, c + 3);
-                }
-                const half8 q0 = c < kW64QRegs ? qop[0][c < kW64QRegs ? c : 0] : qop_l[c & 3][0];
-                const half8 q1 = c < kW64QRegs ? qop[1][c < kW64QRegs ? c : 0] : qop_l[c & 3][1];
-                // each step's vector work is tied behind its MFMA (after_mfma)
+                    for (int rb = 0; rb < 2; rb++) qop_l[(c + 2) % 3][rb] = qop_at(rb, c + 2);
+                const half8 q0 = c < kW64QRegs ? qop[0][c < kW64QRegs ? c : 0] : qop_l[c % 3][0];
+                const half8 q1 = c < kW64QRegs ? qop[1][c < kW64QRegs ? c : 0] : qop_l[c % 3][1];
+                // each step's vector work lies between its MFMA (after_mfma on its inputs) and the
+                // next one (before_mfma on its results)
+                auto gap = [&](int rb) __attribute__((always_inline)) {
+                    const int cz = kAhead ? (c < 15 ? c + 1 : 15) : c;
+                    float z = sp[rb][cz];
+                    after_mfma(z, lsum[rb]);
+                    sp[rb][cz] = z;
+                    float e;
+                    if constexpr (kAhead) {
+                        e = ex[rb];
+                        if (c < 15) ex[rb] = __builtin_amdgcn_exp2f(z);
+                    } else {
+                        e = __builtin_amdgcn_exp2f(z);
+                    }
+                    const uint32_t d = exp_elem(rb, c, e, vq[(c >> 2) & 1], pw, lsum, prv);
+                    before_mfma(lsum[rb], ex[rb], d);
+                };
                 if (c == 0)
                     s_mfma_first(sc[0], kop[c & 3], q0);
                 else
                     s_mfma(sc[0], kop[c & 3], q0);
-                {
-                    // the input of the step's exponential follows the MFMA, the previous step's row
-                    // sum precedes it
-                    const int cz = kAhead ? (c < 15 ? c + 1 : 15) : c;
-                    float z = sp[0][cz];
-                    after_mfma(z, lsum[1]);
-                    sp[0][cz] = z;
-                }
-                if constexpr (kAhead) {
-                    const float e = ex[0];
-                    if (c < 15) ex[0] = __builtin_amdgcn_exp2f(sp[0][c + 1]);
-                    exp_elem(0, c, e, v4, pn, lsum);
-                } else {
-                    exp_elem(0, c, __builtin_amdgcn_exp2f(sp[0][c]), v4, pn, lsum);
-                }
+                gap(0);
                 if (c == 0)
                     s_mfma_first(sc[1], kop[c & 3], q1);
                 else if (c < 15)
                     s_mfma(sc[1], kop[c & 3], q1);
                 else
                     s_mfma_last(sc[1], kop[c & 3], q1);
-                {
-                    const int cz = kAhead ? (c < 15 ? c + 1 : 15) : c;
-                    float z = sp[1][cz];
-                    after_mfma(z, lsum[0]);
-                    sp[1][cz] = z;
-                }
-                if constexpr (kAhead) {
-                    const float e = ex[1];
-                    if (c < 15) ex[1] = __builtin_amdgcn_exp2f(sp[1][c + 1]);
-                    exp_elem(1, c, e, v4, pn, lsum);
-                } else {
-                    exp_elem(1, c, __builtin_amdgcn_exp2f(sp[1][c]), v4, pn, lsum);
-                }
+                gap(1);
             }
         }
 #pragma unroll
         for (int rb = 0; rb < 2; rb++) {
+#pragma unroll
+            for (int u = 0; u < 2; u++)
+                pn[rb][u] = __builtin_bit_cast(half8, make_uint4(pw[rb][4 * u], pw[rb][4 * u + 1], pw[rb][4 * u + 2], pw[rb][4 * u + 3]));
             l[rb] = fmaf(l[rb], dec[rb], lsum[rb]);
             // P(n - 1) complete here, before the barrier: phase B's assembly MFMAs read it, and
             // the compiler pads no wait states for them
@@ -518,31 +586,34 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
 
     // Phase B of tile n: O += V(n - 1)^T P(n - 1) (V operands read kW64VAhead steps ahead),
     // interleaved with S(n)'s scaling (K scale, log2(e) / 16, less the running maximum) and its row
-    // maxima. `need` reports the rows whose maximum grows by more than 2^8 (or that meet their
+    // maxima. `need` reports the rows whose maximum grows by more than 2^15 (or that meet their
     // first key): fix_softmax handles those and the causal mask. One code path for every tile (the
     // accumulators must not meet branches): before the first tile P is zero and the V buffer it
     // reads is zero-filled; after the last (past), S is -inf, which leaves m, l and P unchanged.
     auto phase_b = [&](int n, floatx16 (&sc)[2], const half8 (&pp)[2][2], bool (&need)[2], float (&ymax)[2], bool past,
-                       Raw &raw, const float4 (&k4pre)[4], const half8 (&vpre_in)[kW64VAhead]) __attribute__((always_inline)) {
+                       Raw &raw, const float4 (&k4pre)[4], const half8 (&vpre_in)[kW64VAhead], float4 &v4n,
+                       half8 (&kopn)[3]) __attribute__((always_inline)) {
         float4 k4own[4];
         half8 vown[kW64VAhead];
-        if constexpr (!kEarly) prefetch_b(n, k4own, vown);
+        if constexpr (!kEarly) prefetch_b(k4own, vown);
         const float4 (&k4)[4] = kEarly ? k4pre : k4own;
         const half8 (&vpre)[kW64VAhead] = kEarly ? vpre_in : vown;
         const uint32_t key2 = kbeg + (uint32_t)(n + 2) * kW64Keys;
-        W64KTile &kdst = kbuf[n & 1];                 // tile n's, read in phase A of tile n
-        W64VTile &vdst = vbuf[(n + 2) % kW64VBufs];   // tile n - 2's, read in phase B of tile n - 1
+        W64KTile &kdst = ktile(kcur);   // tile n's, read in phase A of tile n
+        W64VTile &vdst = vtile(vc2);    // tile n - 2's, read in phase B of tile n - 1
         float add[2];
+        float mq[2] = {m[0], m[1]};
+        asm volatile("" : "+v"(mq[0]), "+v"(mq[1]));   // computed in this phase, not hoisted into phase A
 #pragma unroll
         for (int rb = 0; rb < 2; rb++)   // past the last tile: -inf for every key, whatever the (finite) S and K scales
-            add[rb] = past ? -INFINITY : -(m[rb] == -INFINITY ? 0.0f : m[rb]);
+            add[rb] = past ? -INFINITY : -(mq[rb] == -INFINITY ? 0.0f : mq[rb]);
         // step j < 8 scales elements 2j, 2j + 1 of each row block; steps 8-9 take the maxima
         auto scale_pair = [&](int rb, int j) __attribute__((always_inline)) {
-            float x = sc[rb][2 * j], y = sc[rb][2 * j + 1];
-            after_mfma(x, y);
+            // in place, held before the next MFMA (a tie on copies of the inputs would add moves)
             const float4 &kq = k4[j >> 1];
-            sc[rb][2 * j] = fmaf(x, (j & 1) ? kq.z : kq.x, add[rb]);
-            sc[rb][2 * j + 1] = fmaf(y, (j & 1) ? kq.w : kq.y, add[rb]);
+            sc[rb][2 * j] = fmaf(sc[rb][2 * j], (j & 1) ? kq.z : kq.x, add[rb]);
+            sc[rb][2 * j + 1] = fmaf(sc[rb][2 * j + 1], (j & 1) ? kq.w : kq.y, add[rb]);
+            before_mfma(sc[rb][2 * j], sc[rb][2 * j + 1]);
         };
         float mpart[2][2];
         auto max_piece = [&](int rb, int j) __attribute__((always_inline)) {
@@ -550,40 +621,62 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
             if (j == 8) {
                 mpart[rb][0] = max3f(max3f(t[0], t[1], t[2]), max3f(t[3], t[4], t[5]), max3f(t[6], t[7], t[8]));
                 mpart[rb][1] = max3f(max3f(t[9], t[10], t[11]), max3f(t[12], t[13], t[14]), t[15]);
+                before_mfma(mpart[rb][0], mpart[rb][1]);
             } else if (j == 9) {
                 ymax[rb] = pair_max(max3f(mpart[rb][0], mpart[rb][1], mpart[rb][1]));
-                need[rb] = (ymax[rb] > 8.0f) | ((m[rb] == -INFINITY) & (ymax[rb] > -INFINITY));   // no branch
+                need[rb] = ymax[rb] > thr[rb];   // > kRebase, or a row's first keys (thr = -inf while m is)
             }
         };
+        uint32_t xs[4], key3 = 0;
+        uint4 hs;
         half8 vring[kW64VAhead + 1];
 #pragma unroll
         for (int j = 0; j < kW64VAhead; j++) vring[j] = vpre[j];
 #pragma unroll
         for (int j = 0; j < 16; j++) {
-            if (j + kW64VAhead < 16) vring[(j + kW64VAhead) % (kW64VAhead + 1)] = vop(n, j + kW64VAhead);
+            if (j + kW64VAhead < 16) vring[(j + kW64VAhead) % (kW64VAhead + 1)] = vop(j + kW64VAhead);
             const half8 va = vring[j % (kW64VAhead + 1)];
+            // Work per gap (about seven instructions beside each MFMA): steps 0-7 scale two S
+            // elements per row block; step 3 stages the scales of tile n + 2, steps 4-11 its pieces
+            // j - 4 (INT8: one word of codes per gap); the loads of tile n + 3 follow as their
+            // registers free up (scales at step 4, K codes at 8, V codes at 12), about a tile
+            // before their use; steps 12-13 take the maxima; step 14 issues phase A's first reads
+            // of tile n + 1.
             o_mfma(o[0][j & 7], va, pp[0][j >> 3]);
             if (j < 8) scale_pair(0, j);
-            else max_piece(0, j);
-            if (j >= 4 && j < 12) {   // staging of tile n + 2 (past the split: buffers no phase reads)
+            if (j >= 12) max_piece(0, j - 4);
+            if (kInt8 && j >= 4 && j < 12) {   // (the conversion is volatile assembly: it stays in this gap)
+                piece_words(raw, j - 4, xs);
+                i8x4_to_f16_sdwa(xs[0], hs.x, hs.y);
+            }
+            if (!kInt8 && j >= 4 && j < 12) {   // FP16: the whole piece (copies and V^T transposes)
                 uint32_t x[4];
                 piece_words(raw, j - 4, x);
-                if (kInt8)
-                    after_mfma(x[0], x[1]);
-                else
-                    after_mfma(x[0], x[1], x[2], x[3]);
+                after_mfma(x[0], x[1], x[2], x[3]);
                 stage_piece(kdst, vdst, j - 4, x);
             }
-            if (j == 12) stage_scales(vdst, key2, raw);
+            if (j == 3) stage_scales(vdst, key2, raw);
+            if (j == 8) load_part(raw, key3, 1);    // K codes of tile n + 3
+            if (j == 12) load_part(raw, key3, 2);   // V codes of tile n + 3
             o_mfma(o[1][j & 7], va, pp[1][j >> 3]);
             if (j < 8) scale_pair(1, j);
-            else max_piece(1, j);
-            if (j == 13) raw = load_raw(key2 + kW64Keys);   // the codes of tile n + 3
+            if (j >= 12) max_piece(1, j - 4);
+            if (kInt8 && j >= 4 && j < 12) {
+                i8x4_to_f16_sdwa(xs[1], hs.z, hs.w);
+                store_piece(kdst, vdst, j - 4, hs);
+            }
+            if (j == 4) {
+                key3 = min(key2 + kW64Keys, last_key0);   // once per tile; its arithmetic stays here
+                asm volatile("" : "+s"(key3));
+                load_part(raw, key3, 0);   // scales of tile n + 3
+            }
+            if (kEarly && j == 14) prefetch_a(kcur ^ kKT, vc0, v4n, kopn);   // after the last tile: unused reads
         }
     };
 
     // The general case of tile n, after phase B: the causal mask, the lazy running maximum (a row
-    // rebases only when its maximum grows by more than 2^8, so exponentials stay <= 256): S is
+    // rebases only when its maximum grows by more than 2^kRebase, so exponentials stay <= 2^15 and
+    // P in FP16 range; a rebase rescales O, so rarer ones save most of that work): S is
     // shifted by the rebase, `dec` is the factor l takes before tile n's sum joins it.
     // `rescale_row` reports the rows whose O must take dec: a rebase of a row that had keys before.
     // A row's first rebase finds O zero; any other takes dec, also where exp2(-ymax) underflows to 0
@@ -602,11 +695,12 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
         }
 #pragma unroll
         for (int rb = 0; rb < 2; rb++) {
-            const bool rebase = ymax[rb] > 8.0f || (m[rb] == -INFINITY && ymax[rb] > -INFINITY);
+            const bool rebase = ymax[rb] > kRebase || (m[rb] == -INFINITY && ymax[rb] > -INFINITY);
             const float mref = m[rb] == -INFINITY ? 0.0f : m[rb];
             dec[rb] = rebase ? (m[rb] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(-ymax[rb])) : 1.0f;
             rescale_row[rb] = rebase && m[rb] != -INFINITY;
             m[rb] = rebase ? mref + ymax[rb] : m[rb];
+            thr[rb] = m[rb] == -INFINITY ? -INFINITY : kRebase;
             if (rebase) {
 #pragma unroll
                 for (int v = 0; v < 16; v++) sc[rb][v] = sc[rb][v] - ymax[rb];
@@ -643,9 +737,9 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
     for (int rb = 0; rb < 2; rb++)
 #pragma unroll
         for (int v = 0; v < 16; v++) sp[rb][v] = -INFINITY;
-    float4 v4n[4];
+    float4 v4n;
     half8 kopn[3];
-    if constexpr (kEarly) prefetch_a(0, v4n, kopn);
+    if constexpr (kEarly) prefetch_a(kcur, vm1, v4n, kopn);
     for (int n = 0; n <= ntiles; n++) {
         // the accumulators live in the accumulator registers across iterations
 #pragma unroll
@@ -662,19 +756,21 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
         half8 vpre[kW64VAhead];
         if constexpr (kEarly) {
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            prefetch_b(n, k4, vpre);
+            prefetch_b(k4, vpre);
             asm volatile("s_barrier" ::: "memory");
+            // odd waves start phase B half an MFMA step later: the waves run in step after the
+            // barrier, and an LDS write holds its wave until the LDS has taken it, so staging
+            // writes issued by all four at once wait on each other (measured 1.9% per tile)
+            if (wave & 1) asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7");
         } else {
             __syncthreads();
         }
         bool need[2];
         float ymax[2];
-        phase_b(n, sc, pb, need, ymax, n == ntiles, raw, k4, vpre);
-        // after the last tile: unused reads of buffers in range
-        if constexpr (kEarly) prefetch_a(n + 1, v4n, kopn);
+        phase_b(n, sc, pb, need, ymax, n == ntiles, raw, k4, vpre, v4n, kopn);
         dec[0] = dec[1] = 1.0f;
         const bool masked = kbeg + (uint32_t)n * kW64Keys + kW64Keys - 1 > wave_min_limit;
-        if (masked | (__ballot(need[0] | need[1]) != 0)) {   // bitwise: both sides computed
+        if (masked | ((__ballot(need[0]) | __ballot(need[1])) != 0)) {   // bitwise: both sides computed
             bool rescale_row[2];
             fix_softmax(n, sc, ymax, dec, rescale_row, masked);
             // a rebase scales what O holds (through tile n - 1) before P(n) joins it (rows that do
@@ -683,6 +779,12 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
         }
 #pragma unroll
         for (int rb = 0; rb < 2; rb++) sp[rb] = sc[rb];
+        kcur ^= kKT;
+        const uint32_t t = vm1;
+        vm1 = vc0;
+        vc0 = vc1;
+        vc1 = vc2;
+        vc2 = t;
     }
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");   // the last MFMAs' results, before O is read
 #pragma unroll

@@ -29,11 +29,15 @@ __device__ inline void i8x4_to_f16(uint32_t w, uint32_t &lo, uint32_t &hi) {
 
 // The same conversion in four instructions: each converts one byte, sign-extended by the
 // operand select (SDWA), from INT16 to FP16 and writes one half of its destination, the
-// second keeping the half the first wrote. Exact: every INT8 value is an FP16 integer.
+// second write of a destination keeping the half the first wrote. The two destinations
+// alternate, so no instruction reads a register its direct predecessor wrote with a half
+// select (a dst_sel result may reach the next VALU unshifted). Volatile, so that it keeps
+// its place among the assembly MFMAs. Exact: every INT8 value is an FP16 integer.
 __device__ inline void i8x4_to_f16_sdwa(uint32_t w, uint32_t &lo, uint32_t &hi) {
-    asm("v_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
-        "v_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1\n\t"
+    asm volatile(
+        "v_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
         "v_cvt_f16_i16_sdwa %1, sext(%2) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_2\n\t"
+        "v_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1\n\t"
         "v_cvt_f16_i16_sdwa %1, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_3"
         : "=&v"(lo), "=&v"(hi)
         : "v"(w));
