@@ -351,9 +351,9 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
     };
 
     // ---- prologue: the V scales of the split (vs_ref), tile 0's codes, the query
-    float vsv[8];
+    float vsv[16];   // the V scales of the split's first 4096 keys, loaded with the tile codes and the query
 #pragma unroll
-    for (int it = 0; it < 8; it++) {
+    for (int it = 0; it < 16; it++) {
         const uint32_t key = kbeg + tid + 256 * it;
         vsv[it] = kInt8 && key < kend ? p.vs[(size_t)key * 2 + g] : 0.0f;
     }
@@ -370,9 +370,18 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
     }
     float vs_ref = kInt8 ? 0.0f : 1.0f;   // FP16 KV: no V scales
 #pragma unroll
-    for (int it = 0; it < 8; it++) vs_ref = fmaxf(vs_ref, vsv[it]);
-    if (kInt8)
-        for (uint32_t key = kbeg + tid + 2048; key < kend; key += 256) vs_ref = fmaxf(vs_ref, p.vs[(size_t)key * 2 + g]);
+    for (int it = 0; it < 16; it++) vs_ref = fmaxf(vs_ref, vsv[it]);
+    if (kInt8)   // the rest of the split, eight loads in flight per thread (not one round trip per key)
+        for (uint32_t k0 = kbeg + tid + 4096; k0 < kend; k0 += 2048) {
+            float v8[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const uint32_t key = k0 + 256 * u;
+                v8[u] = key < kend ? p.vs[(size_t)key * 2 + g] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) vs_ref = fmaxf(vs_ref, v8[u]);
+        }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) vs_ref = fmaxf(vs_ref, __shfl_xor(vs_ref, o, 64));
     if (lane == 0) vs_partial[wave] = vs_ref;
