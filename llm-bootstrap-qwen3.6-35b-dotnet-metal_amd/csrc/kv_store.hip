@@ -114,9 +114,9 @@ __global__ __launch_bounds__(256) void kv_store_int8_kernel(
                                    vt, 0.0f);
 }
 
-// batch_rope_int8 (kernels.metal:142-146): blocks [0, qblocks) rotate the
-// 16 query heads of every row into qr; the remaining blocks rotate K and
-// append K/V tiles. One launch.
+// batch_rope_int8 (kernels.metal:142-146): the first blocks rotate K and append
+// the K/V tiles; the last qblocks rotate the 16 query heads of every row into
+// qr. One launch.
 __global__ __launch_bounds__(256) void batch_rope_int8_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
     float *__restrict__ qr, int8_t *__restrict__ kc, int8_t *__restrict__ vc,
@@ -124,10 +124,11 @@ __global__ __launch_bounds__(256) void batch_rope_int8_kernel(
     uint32_t qblocks, uint32_t first_tile) {
     __shared__ __attribute__((aligned(16))) uint8_t vt[256 * vt_stride<kTile>()];
     const float ifreq = lane_inv_freq(freq);
-    if (blockIdx.x < qblocks) {
+    const uint32_t kvblocks = gridDim.x - qblocks;   // K/V tiles first, as prepare_fused_int8_kernel
+    if (blockIdx.x >= kvblocks) {
         // one work-group per row, wave w rotating heads 4w..4w+3 (loads issued together)
         const int lane = threadIdx.x & 63, h0 = 4 * (threadIdx.x >> 6);
-        const uint32_t row = blockIdx.x;
+        const uint32_t row = blockIdx.x - kvblocks;
         const Rope4 r = rope_angles(pos + row, lane, ifreq);
         const float *src = q + (size_t)row * 4096 + h0 * 256 + 4 * lane;
         float *dst = qr + (size_t)row * 4096 + h0 * 256 + 4 * lane;
@@ -138,7 +139,7 @@ __global__ __launch_bounds__(256) void batch_rope_int8_kernel(
         for (int h = 0; h < 4; h++) *reinterpret_cast<float4 *>(dst + h * 256) = rope4(x[h], lane, r);
         return;
     }
-    const uint32_t b = blockIdx.x - qblocks;
+    const uint32_t b = blockIdx.x;
     store_tile<true>(k, v, kc, vc, ks, vs, rows, pos, first_tile + b / 2, b & 1, vt, ifreq);
 }
 
@@ -183,11 +184,14 @@ __global__ __launch_bounds__(256) void prepare_fused_int8_kernel(
     uint32_t first_tile) {
     __shared__ __attribute__((aligned(16))) uint8_t vt[256 * vt_stride<kTile>()];
     const float ifreq = lane_inv_freq(freq);
-    if (blockIdx.x < qblocks) {
-        prepare_query_heads(qkv, qw, packed, gate, rows, blockIdx.x, pos, eps, ifreq);
+    // The K/V tiles come first in the grid: their chain (loads, norm, RoPE, two wave maxima, the
+    // V transpose) is the launch's longest, and dispatched behind the query rows they ran last.
+    const uint32_t kvblocks = gridDim.x - qblocks;
+    if (blockIdx.x >= kvblocks) {
+        prepare_query_heads(qkv, qw, packed, gate, rows, blockIdx.x - kvblocks, pos, eps, ifreq);
         return;
     }
-    const uint32_t b = blockIdx.x - qblocks;
+    const uint32_t b = blockIdx.x;
     store_tile<true, true>(k, v, kc, vc, ks, vs, rows, pos, first_tile + b / 2, b & 1, vt, ifreq, KNorm{kw, eps});
 }
 
