@@ -350,6 +350,11 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
         stage_scales(vb, key0, r);
     };
 
+    // INT8: V(n + 1) is staged in phase A of tile n (its buffer's previous tile, n - 3, was last read
+    // in phase B of tile n - 2, before the last barrier), K(n + 2) in phase B of tile n, so each
+    // phase writes half of the tile's LDS (a CU takes LDS writes at a third of its read rate, and
+    // a write holds its wave until then)
+    constexpr bool kVinA = kInt8;
     // ---- prologue: the V scales of the split (vs_ref), tile 0's codes, the query
     float vsv[16];   // the V scales of the split's first 4096 keys, loaded with the tile codes and the query
 #pragma unroll
@@ -391,14 +396,34 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
     vs_inv = __builtin_bit_cast(
         float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(uint32_t, vs_ref > 0.0f ? 1.0f / vs_ref : 0.0f)));
     stage(kbuf[0], vbuf[0], kbeg, raw0);
-    stage(kbuf[1], vbuf[1], kbeg + kW64Keys, raw1);
+    if constexpr (kVinA) {   // tile 1's V waits for phase A of tile 0
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            uint32_t x[4];
+            piece_words(raw1, j, x);
+            stage_piece(kbuf[1], vbuf[1], j, x);
+        }
+        stage_scales(vbuf[1], kbeg + kW64Keys, raw1);
+    } else {
+        stage(kbuf[1], vbuf[1], kbeg + kW64Keys, raw1);
+    }
     // the query chunks are in their registers before the loop (a use here makes the compiler wait
     // for their loads once, instead of before their MFMAs on every tile)
 #pragma unroll
     for (int rb = 0; rb < 2; rb++)
 #pragma unroll
         for (int c = 0; c < kW64QRegs; c++) asm volatile("" ::"v"(qop[rb][c]));
-    Raw raw = load_raw(kbeg + 2 * kW64Keys);   // staged in phase B of tile 0
+    // staged in phase B of tile 0 (INT8: its K and scales; the V codes held are tile 1's)
+    Raw raw;
+    if constexpr (kVinA) {
+        raw.w[2] = raw1.w[2];
+        raw.w[3] = raw1.w[3];
+        const uint32_t key = min(kbeg + 2 * kW64Keys, last_key0);
+        load_part(raw, key, 0);
+        load_part(raw, key, 1);
+    } else {
+        raw = load_raw(kbeg + 2 * kW64Keys);
+    }
     {
         // "tile -1", whose zero probabilities the first PV multiplies: zero V^T codes and scales,
         // not NaN
@@ -508,7 +533,13 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
     // the split, an S that phase B replaces with -inf. v4 (the V scales of tile n - 1) and the
     // first three K operands come from prefetch_a.
     auto phase_a = [&](int n, floatx16 (&sc)[2], floatx16 (&sp)[2], const float (&dec)[2], half8 (&pn)[2][2],
-                       const float4 &v0pre, const half8 (&kpre_in)[3]) __attribute__((always_inline)) {
+                       const float4 &v0pre, const half8 (&kpre_in)[3], Raw &raw) __attribute__((always_inline)) {
+        // INT8: V(n + 1) from the codes in raw, a half-word per step in the gaps of row block 0
+        // (piece 4 + c / 4: word (c / 2) % 2, low or high halves by c % 2), then its codes reloaded
+        // for tile n + 2
+        W64VTile &vnext = vtile(vc1);
+        uint32_t vw[2] = {0u, 0u};
+        uint4 vh = make_uint4(0u, 0u, 0u, 0u);
         float4 v0own;
         half8 kown[3];
         if constexpr (!kEarly) prefetch_a(kcur, vm1, v0own, kown);
@@ -566,6 +597,22 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
                 else
                     s_mfma(sc[0], kop[c & 3], q0);
                 gap(0);
+                if constexpr (kVinA) {
+                    const int piece = 4 + c / 4, sub = c & 3;
+                    if (sub == 0) {
+                        uint32_t x[4];
+                        piece_words(raw, piece, x);
+                        vw[0] = x[0];
+                        vw[1] = x[1];
+                    }
+                    if (sub == 0) i8x4_to_f16_sdwa_lo(vw[0], vh.x, vh.y);
+                    if (sub == 1) i8x4_to_f16_sdwa_hi(vw[0], vh.x, vh.y);
+                    if (sub == 2) i8x4_to_f16_sdwa_lo(vw[1], vh.z, vh.w);
+                    if (sub == 3) {
+                        i8x4_to_f16_sdwa_hi(vw[1], vh.z, vh.w);
+                        store_piece(kbuf[0], vnext, piece, vh);   // (a V piece: the K tile is not touched)
+                    }
+                }
                 if (c == 0)
                     s_mfma_first(sc[1], kop[c & 3], q1);
                 else if (c < 15)
@@ -575,6 +622,7 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
                 gap(1);
             }
         }
+        if constexpr (kVinA) load_part(raw, min(kbeg + (uint32_t)(n + 2) * kW64Keys, last_key0), 2);
 #pragma unroll
         for (int rb = 0; rb < 2; rb++) {
 #pragma unroll
@@ -646,16 +694,19 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
             if (j + kW64VAhead < 16) vring[(j + kW64VAhead) % (kW64VAhead + 1)] = vop(j + kW64VAhead);
             const half8 va = vring[j % (kW64VAhead + 1)];
             // Work per gap (about seven instructions beside each MFMA): steps 0-7 scale two S
-            // elements per row block; step 3 stages the scales of tile n + 2, steps 4-11 its pieces
-            // j - 4 (INT8: one word of codes per gap); the loads of tile n + 3 follow as their
-            // registers free up (scales at step 4, K codes at 8, V codes at 12), about a tile
-            // before their use; steps 12-13 take the maxima; step 14 issues phase A's first reads
-            // of tile n + 1.
+            // elements per row block; step 3 stages the scales of tile n + 2, and its pieces follow
+            // (INT8: the K pieces 0-3 at steps 4, 6, 8, 10, one word of codes per gap — its V is
+            // staged in phase A; FP16: pieces j - 4 at steps 4-11); the loads of tile n + 3 follow
+            // as their registers free up (scales at step 4, K codes after the last K piece, FP16 V
+            // codes at 12), about a tile before their use; steps 12-13 take the maxima; step 14
+            // issues phase A's first reads of tile n + 1.
+            const bool kstep = kInt8 && j >= 4 && j < 12 && (j & 1) == 0;
+            const int kpiece = (j - 4) >> 1;
             o_mfma(o[0][j & 7], va, pp[0][j >> 3]);
             if (j < 8) scale_pair(0, j);
             if (j >= 12) max_piece(0, j - 4);
-            if (kInt8 && j >= 4 && j < 12) {   // (the conversion is volatile assembly: it stays in this gap)
-                piece_words(raw, j - 4, xs);
+            if (kstep) {   // (the conversion is volatile assembly: it stays in this gap)
+                piece_words(raw, kpiece, xs);
                 i8x4_to_f16_sdwa(xs[0], hs.x, hs.y);
             }
             if (!kInt8 && j >= 4 && j < 12) {   // FP16: the whole piece (copies and V^T transposes)
@@ -665,14 +716,14 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
                 stage_piece(kdst, vdst, j - 4, x);
             }
             if (j == 3) stage_scales(vdst, key2, raw);
-            if (j == 8) load_part(raw, key3, 1);    // K codes of tile n + 3
-            if (j == 12) load_part(raw, key3, 2);   // V codes of tile n + 3
+            if (j == (kVinA ? 12 : 8)) load_part(raw, key3, 1);   // K codes of tile n + 3
+            if (!kVinA && j == 12) load_part(raw, key3, 2);        // V codes of tile n + 3
             o_mfma(o[1][j & 7], va, pp[1][j >> 3]);
             if (j < 8) scale_pair(1, j);
             if (j >= 12) max_piece(1, j - 4);
-            if (kInt8 && j >= 4 && j < 12) {
+            if (kstep) {
                 i8x4_to_f16_sdwa(xs[1], hs.z, hs.w);
-                store_piece(kdst, vdst, j - 4, hs);
+                store_piece(kdst, vdst, kpiece, hs);
             }
             if (j == 4) {
                 key3 = min(key2 + kW64Keys, last_key0);   // once per tile; its arithmetic stays here
@@ -756,7 +807,7 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
 #pragma unroll
             for (int dt = 0; dt < 8; dt++) asm volatile("" : "+a"(o[rb][dt]));
         floatx16 sc[2];
-        phase_a(n, sc, sp, dec, pb, v4n, kopn);
+        phase_a(n, sc, sp, dec, pb, v4n, kopn, raw);
         // The barrier between the phases, with phase B's first reads in flight across it: this
         // wave's LDS writes (the staging of phase B of tile n - 1) and phase A's reads are complete
         // first, as a work-group barrier's release would have them, and the assembly barrier keeps

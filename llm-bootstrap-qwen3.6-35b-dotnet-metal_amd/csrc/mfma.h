@@ -43,6 +43,24 @@ __device__ inline void i8x4_to_f16_sdwa(uint32_t w, uint32_t &lo, uint32_t &hi) 
         : "v"(w));
 }
 
+// The same conversion in two halves, for code that spreads it over several places: _lo writes
+// bytes 0 and 2 into the low halves of lo and hi, _hi bytes 1 and 3 into their high halves
+// (keeping the low ones). Between the two, lo and hi hold half-written words.
+__device__ inline void i8x4_to_f16_sdwa_lo(uint32_t w, uint32_t &lo, uint32_t &hi) {
+    asm volatile(
+        "v_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+        "v_cvt_f16_i16_sdwa %1, sext(%2) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_2"
+        : "=&v"(lo), "=&v"(hi)
+        : "v"(w));
+}
+__device__ inline void i8x4_to_f16_sdwa_hi(uint32_t w, uint32_t &lo, uint32_t &hi) {
+    asm volatile(
+        "v_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1\n\t"
+        "v_cvt_f16_i16_sdwa %1, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_3"
+        : "+v"(lo), "+v"(hi)
+        : "v"(w));
+}
+
 // Eight INT8 codes (two dwords) -> half8 operand, in byte order.
 __device__ inline half8 i8x8_to_half8(uint32_t w0, uint32_t w1) {
     uint32_t r[4];
