@@ -355,14 +355,38 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
     // phase writes half of the tile's LDS (a CU takes LDS writes at a third of its read rate, and
     // a write holds its wave until then)
     constexpr bool kVinA = kInt8;
-    // ---- prologue: the V scales of the split (vs_ref), tile 0's codes, the query
-    float vsv[16];   // the V scales of the split's first 4096 keys, loaded with the tile codes and the query
+    // ---- prologue: the query, the V scales of the split (vs_ref), tile 0's codes. The query
+    // chunks kept in LDS go first and straight into LDS (global_load_lds_dwordx4: lane l's 16
+    // bytes to the wave's base in M0 + 16 l), holding no registers in flight. They are issued in
+    // assembly, unseen by the compiler's counter bookkeeping: a compiler-issued LDS load makes it
+    // wait for every load before each use of any of them, while these, the oldest, have simply
+    // landed whenever a later load has (the counter counts in order). The V scales, the codes of
+    // tiles 0 and 1, and the register chunks of the query follow, in the order of first use, so
+    // that the V-scale maximum, its barrier and the staging run while the last of them are in
+    // flight. (The empty assembly statements keep the compiler from reordering the groups.)
+#pragma unroll
+    for (int rb = 0; rb < 2; rb++) {
+        const uint32_t rr = row_valid[rb] ? my_row[rb] : R - 1;
+        const _Float16 *qrow = p.q + ((size_t)g * R + rr) * 256 + 8 * kk;
+#pragma unroll
+        for (int c = kW64QRegs; c < 16; c++) {
+            const uint32_t lds = (uint32_t)(uintptr_t)&qlds[c - kW64QRegs][rb][64 * wave];   // wave-uniform
+            uint32_t saved;
+            asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %2, off\n\ts_mov_b32 m0, %0"
+                         : "=&s"(saved)
+                         : "s"(lds), "v"(qrow + 16 * c)
+                         : "memory");
+        }
+    }
+    float vsv[16];   // the V scales of the split's first 4096 keys
 #pragma unroll
     for (int it = 0; it < 16; it++) {
         const uint32_t key = kbeg + tid + 256 * it;
         vsv[it] = kInt8 && key < kend ? p.vs[(size_t)key * 2 + g] : 0.0f;
     }
+    asm volatile("" ::: "memory");
     const Raw raw0 = load_raw(kbeg), raw1 = load_raw(kbeg + kW64Keys);
+    asm volatile("" ::: "memory");
     half8 qop[2][kW64QRegs];
 #pragma unroll
     for (int rb = 0; rb < 2; rb++) {
@@ -370,8 +394,6 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
         const _Float16 *qrow = p.q + ((size_t)g * R + rr) * 256 + 8 * kk;
 #pragma unroll
         for (int c = 0; c < kW64QRegs; c++) qop[rb][c] = *reinterpret_cast<const half8 *>(qrow + 16 * c);
-#pragma unroll
-        for (int c = kW64QRegs; c < 16; c++) qlds[c - kW64QRegs][rb][tid] = *reinterpret_cast<const uint4 *>(qrow + 16 * c);
     }
     float vs_ref = kInt8 ? 0.0f : 1.0f;   // FP16 KV: no V scales
 #pragma unroll
@@ -431,6 +453,7 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
         uint4 *z = reinterpret_cast<uint4 *>(&vbuf[kW64VBufs - 1]);
         for (int e = tid; e < (int)(sizeof(W64VTile) / 16); e += 256) z[e] = make_uint4(0, 0, 0, 0);
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the query's LDS chunks have landed
     __syncthreads();
 
     floatx16 o[2][8];
