@@ -61,15 +61,26 @@ __device__ void store_tile(const float *__restrict__ k, const float *__restrict_
 #pragma unroll
             for (int i = 0; i < 4; i++) vx[u][i] = vr[lane + 64 * i];
         }
+        // The four tokens' chains (norm, rotation, two wave maxima: cross-lane steps with memory-like
+        // latency) are computed together, with no branch between them, so that they overlap; only
+        // the stores are skipped for tokens outside [lo, hi) (their loads read an in-range row).
+        float4 kq[4];
+        float kam[4], vam[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            float4 kv = kx[u];
+            if (Norm) kv = rms_norm4(kv, knorm.eps, knorm.w, lane, 1.0f);
+            if (Rope) kv = rope4(kv, lane, rope_angles(tile0 + tb + 4 * u, lane, ifreq));
+            kam[u] = wave_max(fmaxf(fmaxf(fabsf(kv.x), fabsf(kv.y)), fmaxf(fabsf(kv.z), fabsf(kv.w))));
+            vam[u] = wave_max(fmaxf(fmaxf(fabsf(vx[u][0]), fabsf(vx[u][1])), fmaxf(fabsf(vx[u][2]), fabsf(vx[u][3]))));
+            kq[u] = kv;
+        }
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const uint32_t tl = tb + 4 * u, t = tile0 + tl;
             if (t < lo || t >= hi) continue;  // wave-uniform
-            float4 kv = kx[u];
-            if (Norm) kv = rms_norm4(kv, knorm.eps, knorm.w, lane, 1.0f);
-            if (Rope) kv = rope4(kv, lane, rope_angles(t, lane, ifreq));
-            const float ka = wave_max(fmaxf(fmaxf(fabsf(kv.x), fabsf(kv.y)), fmaxf(fabsf(kv.z), fabsf(kv.w))));
-            const float va = wave_max(fmaxf(fmaxf(fabsf(vx[u][0]), fabsf(vx[u][1])), fmaxf(fabsf(vx[u][2]), fabsf(vx[u][3]))));
+            const float4 kv = kq[u];
+            const float ka = kam[u], va = vam[u];
             const uint64_t vector = (uint64_t)t * 2 + h;
             if (lane == 0) {
                 ks[vector] = ka / 127.0f;
