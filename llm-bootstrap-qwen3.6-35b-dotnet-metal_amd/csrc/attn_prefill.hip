@@ -156,11 +156,13 @@ constexpr int kW64Keys = 32;               // keys per tile
 // FP16 (largest 65504); a maximum that lags only makes the kept exponentials larger.
 constexpr float kRebase = 15.0f;
 constexpr int kW64VBufs = 4;               // V^T tiles in LDS
-#ifndef BOOT_W64_QLDS
-#define BOOT_W64_QLDS 7
-#endif
-constexpr int kW64QLds = BOOT_W64_QLDS;    // Q^T chunks per row block kept in LDS, the rest in registers
-constexpr int kW64QRegs = 16 - kW64QLds;
+// Q^T chunks per row block kept in LDS, the rest in registers (phase A reads the LDS ones two
+// steps ahead). The INT8 kernel keeps twelve in registers: from nine to twelve, 3451 -> 3350
+// cycles per tile with no spill. The FP16 control's staging holds more registers and spills
+// beyond nine (3878 -> 4604 cycles with ten). At least four stay in LDS: the epilogue stages one
+// wave's 32 KB of rows in that region.
+template <bool kInt8>
+constexpr int w64_qlds() { return kInt8 ? 4 : 7; }
 #ifndef BOOT_W64_VAHEAD
 #define BOOT_W64_VAHEAD 3
 #endif
@@ -180,7 +182,8 @@ template <bool kInt8>
 __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
     __shared__ W64KTile kbuf[2];
     __shared__ W64VTile vbuf[kW64VBufs];
-    __shared__ uint4 qlds[kW64QLds > 0 ? kW64QLds : 1][2][256];   // [chunk][row block][thread]
+    constexpr int kW64QLds = w64_qlds<kInt8>(), kW64QRegs = 16 - kW64QLds;
+    __shared__ uint4 qlds[kW64QLds][2][256];   // [chunk][row block][thread]
     __shared__ float vs_partial[4];
 
     uint32_t g, tile, split;
