@@ -201,16 +201,21 @@ struct ChunkLds {
     uint4 v[256][8];
 };
 
+// The chunk loads are non-temporal (`nt`): each cache byte is read once per step, so it need not
+// displace anything in L2 (29.5 instead of 30.6-31.1 us per layer step at 131073).
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
 __device__ __attribute__((always_inline)) inline uint4 load_k_piece(const DecodeParams &p, uint32_t g, uint32_t c0,
                                                                     uint32_t length, int tid, int i) {
     const uint32_t t = min(c0 + (uint32_t)(tid >> 4) + 32 * i, length - 1);
-    return *reinterpret_cast<const uint4 *>(p.k + ((size_t)t * 2 + g) * 256 + 16 * (tid & 15));
+    return __builtin_bit_cast(
+        uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p.k + ((size_t)t * 2 + g) * 256 + 16 * (tid & 15))));
 }
 
 // 16 bytes as a value (a struct copy straight from global memory would keep the
 // register set in a stack object)
 __device__ __attribute__((always_inline)) inline uint4 load_piece(const int8_t *at) {
-    return *reinterpret_cast<const uint4 *>(at);
+    return __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(at)));
 }
 
 // K or V of chunk idx of the split starting at token `begin`. Past the last chunk
