@@ -20,6 +20,12 @@
 namespace boot {
 namespace {
 
+// A read-once float4 (non-temporal load: it need not displace anything in L2)
+__device__ __attribute__((always_inline)) inline float4 load_once4(const float *at) {
+    typedef float f32x4_t __attribute__((ext_vector_type(4)));
+    return __builtin_bit_cast(float4, __builtin_nontemporal_load(reinterpret_cast<const f32x4_t *>(at)));
+}
+
 constexpr int kTile = 16;               // tokens per store work-group (page-aligned tiles): 4 per wave
 constexpr int kBulkTile = 64;           // tile of large appends: whole 64-byte V page-row runs
 constexpr uint64_t kBulkRows = 4096;    // appends of at least this many rows use kBulkTile
@@ -57,9 +63,9 @@ __device__ void store_tile(const float *__restrict__ k, const float *__restrict_
             const uint32_t row = t - pos;
             const float *kr = k + ((size_t)row * 2 + h) * 256;
             const float *vr = v + ((size_t)row * 2 + h) * 256;
-            kx[u] = *reinterpret_cast<const float4 *>(kr + 4 * lane);
+            kx[u] = load_once4(kr + 4 * lane);
 #pragma unroll
-            for (int i = 0; i < 4; i++) vx[u][i] = vr[lane + 64 * i];
+            for (int i = 0; i < 4; i++) vx[u][i] = __builtin_nontemporal_load(vr + lane + 64 * i);
         }
         // The four tokens' chains (norm, rotation, two wave maxima: cross-lane steps with memory-like
         // latency) are computed together, with no branch between them, so that they overlap; only
