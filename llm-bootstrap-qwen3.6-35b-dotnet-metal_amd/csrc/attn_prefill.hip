@@ -10,11 +10,17 @@
 //   y = o / l * sigmoid(gate)
 // One deliberate change: the scaled probabilities are rounded to FP16 after
 // dividing the V scales by their maximum over the work-group's key range
-// (vs_ref), and vs_ref multiplies the result once at the end. e * vs / vs_ref
-// lies in [0, 1], so FP16 cannot underflow where it matters (the reason the
-// reference chose BF16, docs/INT8_KV_20261104.md:16) and its rounding is 8x
-// finer than BF16's, which keeps the output within rel-L2 1e-3 of FP64 where
-// BF16 probabilities measure 1.6e-3 to 3.2e-3.
+// (vs_ref) and multiplying them by 2^7, and vs_ref / 2^7 multiplies the result
+// once at the end. e * 2^7 * vs / vs_ref lies in [0, 2^15], so FP16 neither
+// overflows nor drops small probabilities into its subnormals (the reason the
+// reference chose BF16, docs/INT8_KV_20261104.md:16), and its rounding is 8x
+// finer than BF16's. The denominator sums the rounded operands divided back by
+// their factor (P / (2^7 vs / vs_ref), one mixed FP16 x FP32 FMA per element in
+// place of the add of e), so an operand's rounding moves numerator and
+// denominator together: a row dominated by one key returns that key's value
+// exactly, and the remaining error scales with the spread of the values, not
+// their size (heavy-tailed V reaches |y| ~ 16, where a denominator of unrounded
+// e leaves FP16's relative 2^-12 as an absolute error above 2e-3).
 // Logical row r of KV group g is (token r/8, head 8g + r%8): the grouped FP16
 // query layout of attention_query_grouped_half (kernels.metal:1276-1281).
 // The FP16-KV control (attention_online_q32_k256_s8_g8_r2, kernels.metal:1356-1365:
@@ -42,9 +48,15 @@ namespace {
 constexpr int kKStride = 256 + 8;          // FP16 K tile row stride (halves): 528 bytes
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kTileRows = 256;             // logical rows per work-group (32 tokens x 8 heads)
-// Split partial of one work-group: O^T / l per row as FP16 (|value| <= 127: a mean of V
-// codes weighted by V scale / vs_ref <= 1), then m, l and vs_ref per row as floats.
-constexpr size_t kPartialBytes = (size_t)kTileRows * 256 * 2 + 3 * kTileRows * 4;
+// Split partial of one work-group: O^T / l per row in region A ([256 rows][512 B]: the row in FP16,
+// or dimensions 0-127 in FP32) and region B (dimensions 128-255 of FP32 rows; the epilogue chooses
+// the format per wave), then m, l and vs_ref / 2^7 per row as floats, the last negated for FP32
+// rows. FP16 rows, the common case, are as compact as a plain FP16 partial.
+constexpr size_t kPartialRegion = (size_t)kTileRows * 512;
+constexpr size_t kPartialBytes = 2 * kPartialRegion + 3 * kTileRows * 4;
+// A wave's partials are FP16 when its outputs are at most this large (FP16's relative 2^-12 of 4
+// is 9.8e-4), FP32 otherwise.
+constexpr float kNarrowPartial = 4.0f;
 
 struct PrefillParams {
     const _Float16 *q;      // grouped FP16 [2][M][8][256]
@@ -144,7 +156,7 @@ __device__ __forceinline__ void before_mfma(uint32_t x, uint32_t y) { asm volati
 //   B: O += V(n - 1)^T P(n - 1) (32 MFMAs), interleaved with S(n)'s scaling and row maxima, the
 //      staging of tile n + 2 (INT8: codes converted to FP16; FP16: copied, V transposed) and
 //      the loads of tile n + 3.
-// Rows whose maximum grows by more than 2^15, and tiles on the causal diagonal, take a fix-up
+// Rows whose maximum grows by more than 2^8, and tiles on the causal diagonal, take a fix-up
 // after phase B (the general softmax); the common case needs no maximum before exp2. The
 // MFMAs are inline assembly, so that their order, and the operand reads placed three steps
 // ahead of them, are kept; each step's vector work is tied behind its MFMA. K tiles are
@@ -152,15 +164,18 @@ __device__ __forceinline__ void before_mfma(uint32_t x, uint32_t y) { asm volati
 // phase writes was last read before the previous barrier.
 constexpr int kW64Keys = 32;               // keys per tile
 // Lazy running maximum: a row rebases when a tile's maximum exceeds it by more than 2^kRebase
-// (log2 units). Exponentials then stay <= 2^15 = 32768, so P = e * vs / vs_ref (<= e) is finite in
+// (log2 units). Exponentials then stay <= 2^8, so P = e * 2^7 * vs / vs_ref (<= 2^15) is finite in
 // FP16 (largest 65504); a maximum that lags only makes the kept exponentials larger.
-constexpr float kRebase = 15.0f;
+constexpr float kRebase = 8.0f;
+constexpr float kPScale = 128.0f;          // 2^7: the probability operand's factor (see above)
 constexpr int kW64VBufs = 4;               // V^T tiles in LDS
 // Q^T chunks per row block kept in LDS, the rest in registers (phase A reads the LDS ones two
 // steps ahead). The INT8 kernel keeps twelve in registers: from nine to twelve, 3451 -> 3350
-// cycles per tile with no spill. The FP16 control's staging holds more registers and spills
-// beyond nine (3878 -> 4604 cycles with ten). At least four stay in LDS: the epilogue stages one
-// wave's 32 KB of rows in that region.
+// cycles per tile with no spill (the probability factors and their reciprocals are read a key
+// pair at a time, two steps ahead, so the row sums' reciprocals take no registers from them; read
+// four keys at a time and four steps ahead they pushed a query chunk to scratch). The FP16
+// control's staging holds more registers and spills beyond nine (3878 -> 4604 cycles with ten).
+// At least four stay in LDS: the epilogue stages one wave's 32 KB of rows in that region.
 template <bool kInt8>
 constexpr int w64_qlds() { return kInt8 ? 4 : 7; }
 #ifndef BOOT_W64_VAHEAD
@@ -175,7 +190,9 @@ struct W64VTile {
     _Float16 v[256 * kW64Keys];            // V^T codes as FP16: 64-byte dimension rows whose 16-byte
                                            // pieces are XOR-swizzled by (row / 4) % 4
     float ks[kW64Keys];                    // K scale * log2(e) / 16 (0 beyond K)
-    float vs[kW64Keys];                    // V scale / vs_ref (0 beyond K)
+    float4 rv[kW64Keys / 2];               // per key pair: r = 2^7 V scale / vs_ref (2^7 for a zero
+                                           // vector) and 1 / r of each key, {r0, 1/r0, r1, 1/r1}
+                                           // (0 beyond K)
 };
 
 template <bool kInt8>
@@ -337,10 +354,13 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
             float ks = r.ks, vs = r.vs;
             after_mfma(ks, vs);   // the products stay where the call is (not hoisted to the loads)
             vb.ks[t] = inside ? ks * (kLog2e / 16.0f) : 0.0f;
-            vb.vs[t] = inside ? vs * vs_inv : 0.0f;
+            // a zero V vector (codes 0, scale 0) keeps the factor 2^7: its key adds nothing to O but
+            // its weight to the denominator
+            const float r = vs > 0.0f ? vs * vs_inv * kPScale : kPScale;
+            reinterpret_cast<float2 *>(vb.rv)[t] = inside ? make_float2(r, __builtin_amdgcn_rcpf(r)) : make_float2(0.0f, 0.0f);
         } else {
             vb.ks[t] = inside ? kLog2e / 16.0f : 0.0f;
-            vb.vs[t] = inside ? 1.0f : 0.0f;
+            reinterpret_cast<float2 *>(vb.rv)[t] = inside ? make_float2(kPScale, 1.0f / kPScale) : make_float2(0.0f, 0.0f);
         }
     };
     auto stage = [&](W64KTile &kb, W64VTile &vb, uint32_t key0, const Raw &r) __attribute__((always_inline)) {
@@ -489,36 +509,38 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
     constexpr uint32_t kKT = sizeof(W64KTile), kVT = sizeof(W64VTile);
     uint32_t kcur = 0, vm1 = (kW64VBufs - 1) * kVT, vc0 = 0, vc1 = kVT, vc2 = 2 * kVT;   // tile 0
 
-    // the K (or V) scales of a tile's keys, as the softmax lanes hold them
-    auto load_scales = [&](uint32_t vo, bool v, float4 (&x4)[4]) __attribute__((always_inline)) {
-        const W64VTile &sb = vtile(vo);
-        const float *src = v ? sb.vs : sb.ks;
+    // the K scales of a tile's keys, as the softmax lanes hold them (element v of a lane's S row:
+    // key 16 (v / 8) + 8 kk + v % 8)
+    auto load_scales = [&](uint32_t vo, float4 (&x4)[4]) __attribute__((always_inline)) {
+        const float *src = vtile(vo).ks;
 #pragma unroll
         for (int q4 = 0; q4 < 4; q4++)
             x4[q4] = *reinterpret_cast<const float4 *>(src + 16 * (q4 >> 1) + 8 * kk + 4 * (q4 & 1));
     };
-
-    auto load_scale4 = [&](uint32_t vo, bool v, int q4) __attribute__((always_inline)) {
-        const W64VTile &sb = vtile(vo);
-        const float *src = v ? sb.vs : sb.ks;
-        return *reinterpret_cast<const float4 *>(src + 16 * (q4 >> 1) + 8 * kk + 4 * (q4 & 1));
+    // the probability factors and their reciprocals of the key pair of elements v, v + 1 (v even):
+    // {r(v), 1 / r(v), r(v + 1), 1 / r(v + 1)}
+    auto load_rv = [&](uint32_t vo, int v) __attribute__((always_inline)) {
+        return vtile(vo).rv[8 * (v >> 3) + 4 * kk + ((v & 7) >> 1)];
     };
 
     // The softmax of tile n - 1, finished in phase A of tile n: element v of row block rb of
-    // exp2(S) (e, with S scaled and shifted by the running maximum), times the key's V scale /
-    // vs_ref into P (FP16, RNE), and into the row's sum.
+    // exp2(S) (e, with S scaled and shifted by the running maximum), times the key's factor
+    // 2^7 V scale / vs_ref into P (FP16, RNE); the row's sum takes each rounded P times the
+    // factor's reciprocal (a mixed FP16 x FP32 FMA).
     // Elements are packed in pairs as the odd one completes (the product of the even one waits in
     // `prv`), and the pair goes to its P register at once.
     typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-    auto exp_elem = [&](int rb, int v, float e, const float4 &w, uint32_t (&pw)[2][8], float (&lsum)[2],
+    auto exp_elem = [&](int rb, int v, float e, const float4 &rw, uint32_t (&pw)[2][8], float (&lsum)[2],
                         float (&prv)[2]) __attribute__((always_inline)) {
-        const float vsc = (v & 3) == 0 ? w.x : (v & 3) == 1 ? w.y : (v & 3) == 2 ? w.z : w.w;
-        const float prod = e * vsc;
-        lsum[rb] += e;
+        const float prod = e * ((v & 1) ? rw.z : rw.x);
         uint32_t d;
         if (v & 1) {
             const half2_t h = {(_Float16)prv[rb], (_Float16)prod};
             d = __builtin_bit_cast(uint32_t, h);
+            // the sum takes the packed halves themselves (mixed FMAs on the P register), so that it
+            // sees exactly the operands the MFMA multiplies
+            asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel_hi:[1,0,0]" : "+v"(lsum[rb]) : "v"(d), "v"(rw.y));
+            asm("v_fma_mix_f32 %0, %1, %2, %0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(lsum[rb]) : "v"(d), "v"(rw.w));
             pw[rb][v >> 1] = d;
         } else {
             prv[rb] = prod;
@@ -535,8 +557,8 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
     constexpr bool kEarly = kInt8;
     static_assert(kW64QRegs >= 3, "the first three QK steps take their Q^T chunks from registers");
     // (ko, vo: the K tile phase A reads and the V tile whose scales its products take)
-    auto prefetch_a = [&](uint32_t ko, uint32_t vo, float4 &v0, half8 (&kop)[3]) __attribute__((always_inline)) {
-        v0 = load_scale4(vo, true, 0);
+    auto prefetch_a = [&](uint32_t ko, uint32_t vo, float4 &r0, half8 (&kop)[3]) __attribute__((always_inline)) {
+        r0 = load_rv(vo, 0);
         const _Float16 *kr = ktile(ko).k + qk_key_row(i) * kKStride + 8 * kk;
 #pragma unroll
         for (int c = 0; c < 3; c++) kop[c] = *reinterpret_cast<const half8 *>(kr + 16 * c);
@@ -548,7 +570,7 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
         return *reinterpret_cast<const half8 *>(vt + 32 * (j & 7) * kW64Keys + 8 * ((2 * (j >> 3) + kk) ^ vsw));
     };
     auto prefetch_b = [&](float4 (&k4)[4], half8 (&vr)[kW64VAhead]) __attribute__((always_inline)) {
-        load_scales(vc0, false, k4);
+        load_scales(vc0, k4);
 #pragma unroll
         for (int j = 0; j < kW64VAhead; j++) vr[j] = vop(j);
     };
@@ -556,22 +578,23 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
     // Phase A of tile n: S(n) for both row blocks (K operands read three steps ahead) and the
     // exponentials of tile n - 1 (P(n - 1) and l), spread between the MFMAs. One path for every
     // n: after the last tile (n = ntiles) the MFMAs multiply the finite codes staged for keys past
-    // the split, an S that phase B replaces with -inf. v4 (the V scales of tile n - 1) and the
-    // first three K operands come from prefetch_a.
+    // the split, an S that phase B replaces with -inf. r0 (the probability factors of tile n - 1's
+    // first key pair and their reciprocals) and the first three K operands come from prefetch_a.
     auto phase_a = [&](int n, floatx16 (&sc)[2], floatx16 (&sp)[2], const float (&dec)[2], half8 (&pn)[2][2],
-                       const float4 &v0pre, const half8 (&kpre_in)[3], Raw &raw) __attribute__((always_inline)) {
+                       const float4 &r0pre, const half8 (&kpre_in)[3], Raw &raw) __attribute__((always_inline)) {
         // INT8: V(n + 1) from the codes in raw, a half-word per step in the gaps of row block 0
         // (piece 4 + c / 4: word (c / 2) % 2, low or high halves by c % 2), then its codes reloaded
         // for tile n + 2
         W64VTile &vnext = vtile(vc1);
         uint32_t vw[2] = {0u, 0u};
         uint4 vh = make_uint4(0u, 0u, 0u, 0u);
-        float4 v0own;
+        float4 r0own;
         half8 kown[3];
-        if constexpr (!kEarly) prefetch_a(kcur, vm1, v0own, kown);
-        // the V scales of tile n - 1, four keys per read, each read four steps before its use
-        float4 vq[2];
-        vq[0] = kEarly ? v0pre : v0own;
+        if constexpr (!kEarly) prefetch_a(kcur, vm1, r0own, kown);
+        // the probability factors of tile n - 1 and their reciprocals, a key pair per read, each
+        // read two steps before its use
+        float4 rq[2];
+        rq[0] = kEarly ? r0pre : r0own;
         const half8 (&kpre)[3] = kEarly ? kpre_in : kown;
         float lsum[2] = {0.0f, 0.0f};
         // INT8: exp2 runs one step ahead of its use: the wave issues in order, and a product
@@ -595,7 +618,7 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
 #pragma unroll
             for (int c = 0; c < 16; c++) {
                 if (c + 3 < 16) kop[(c + 3) & 3] = *reinterpret_cast<const half8 *>(kr + 16 * (c + 3));
-                if ((c & 3) == 0 && c < 12) vq[((c >> 2) + 1) & 1] = load_scale4(vm1, true, (c >> 2) + 1);
+                if ((c & 1) == 0 && c < 14) rq[((c >> 1) + 1) & 1] = load_rv(vm1, c + 2);
                 if (c + 2 < 16 && c + 2 >= kW64QRegs)
 #pragma unroll
                     for (int rb = 0; rb < 2; rb++) qop_l[(c + 2) % 3][rb] = qop_at(rb, c + 2);
@@ -615,7 +638,7 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
                     } else {
                         e = __builtin_amdgcn_exp2f(z);
                     }
-                    const uint32_t d = exp_elem(rb, c, e, vq[(c >> 2) & 1], pw, lsum, prv);
+                    const uint32_t d = exp_elem(rb, c, e, rq[(c >> 1) & 1], pw, lsum, prv);
                     before_mfma(lsum[rb], ex[rb], d);
                 };
                 if (c == 0)
@@ -674,7 +697,7 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
     // accumulators must not meet branches): before the first tile P is zero and the V buffer it
     // reads is zero-filled; after the last (past), S is -inf, which leaves m, l and P unchanged.
     auto phase_b = [&](int n, floatx16 (&sc)[2], const half8 (&pp)[2][2], bool (&need)[2], float (&ymax)[2], bool past,
-                       Raw &raw, const float4 (&k4pre)[4], const half8 (&vpre_in)[kW64VAhead], float4 &v4n,
+                       Raw &raw, const float4 (&k4pre)[4], const half8 (&vpre_in)[kW64VAhead], float4 &r4n,
                        half8 (&kopn)[3]) __attribute__((always_inline)) {
         float4 k4own[4];
         half8 vown[kW64VAhead];
@@ -756,7 +779,7 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
                 asm volatile("" : "+s"(key3));
                 load_part(raw, key3, 0);   // scales of tile n + 3
             }
-            if (kEarly && j == 14) prefetch_a(kcur ^ kKT, vc0, v4n, kopn);   // after the last tile: unused reads
+            if (kEarly && j == 14) prefetch_a(kcur ^ kKT, vc0, r4n, kopn);   // after the last tile: unused reads
         }
     };
 
@@ -823,9 +846,9 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
     for (int rb = 0; rb < 2; rb++)
 #pragma unroll
         for (int v = 0; v < 16; v++) sp[rb][v] = -INFINITY;
-    float4 v4n;
+    float4 r4n;
     half8 kopn[3];
-    if constexpr (kEarly) prefetch_a(kcur, vm1, v4n, kopn);
+    if constexpr (kEarly) prefetch_a(kcur, vm1, r4n, kopn);
     for (int n = 0; n <= ntiles; n++) {
         // the accumulators live in the accumulator registers across iterations
 #pragma unroll
@@ -833,7 +856,7 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
 #pragma unroll
             for (int dt = 0; dt < 8; dt++) asm volatile("" : "+a"(o[rb][dt]));
         floatx16 sc[2];
-        phase_a(n, sc, sp, dec, pb, v4n, kopn, raw);
+        phase_a(n, sc, sp, dec, pb, r4n, kopn, raw);
         // The barrier between the phases, with phase B's first reads in flight across it: this
         // wave's LDS writes (the staging of phase B of tile n - 1) and phase A's reads are complete
         // first, as a work-group barrier's release would have them, and the assembly barrier keeps
@@ -853,7 +876,7 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
         }
         bool need[2];
         float ymax[2];
-        phase_b(n, sc, pb, need, ymax, n == ntiles, raw, k4, vpre, v4n, kopn);
+        phase_b(n, sc, pb, need, ymax, n == ntiles, raw, k4, vpre, r4n, kopn);
         dec[0] = dec[1] = 1.0f;
         const bool masked = kbeg + (uint32_t)n * kW64Keys + kW64Keys - 1 > wave_min_limit;
         if (masked | ((__ballot(need[0]) | __ballot(need[1])) != 0)) {   // bitwise: both sides computed
@@ -876,14 +899,16 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
 #pragma unroll
     for (int rb = 0; rb < 2; rb++) l[rb] += __shfl_xor(l[rb], 32, 64);   // the two lanes of a row summed disjoint keys
 
-    // ---- epilogue: lane (i, kk) holds O^T[d][row] for d = 32dt + 8(v/4) + 4kk + v%4
+    // ---- epilogue: lane (i, kk) holds O^T[d][row] for d = 32dt + 8(v/4) + 4kk + v%4. O sums the
+    // operands 2^7 e vs / vs_ref times the codes, so vs_ref / 2^7 turns O / l into values.
+    const float vs_out = vs_ref * (1.0f / kPScale);
     if (p.splits == 1) {
 #pragma unroll
         for (int rb = 0; rb < 2; rb++) {
             if (!row_valid[rb]) continue;
             const uint32_t token = my_row[rb] / 8, head = g * 8 + my_row[rb] % 8;
             const size_t base = ((size_t)token * 16 + head) * 256;
-            const float inv = vs_ref / l[rb];
+            const float inv = vs_out / l[rb];
 #pragma unroll
             for (int dt = 0; dt < 8; dt++)
 #pragma unroll
@@ -900,12 +925,17 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
         }
         return;
     }
-    // Split partials: O^T / l as FP16 rows through LDS, so that every store instruction writes
-    // 1 KB of whole rows (16-byte pieces of 32 rows each reach HBM as partial lines). Wave w stages
-    // its 64 rows (32 KB, 16-byte chunks XOR-swizzled by row) in a region no other wave uses:
-    // K tiles, V tiles 0-1, V tiles 2-3, the Q^T chunks.
+    // Split partials: O^T / l per row, through LDS so that every store instruction writes 1 KB
+    // of whole rows (16-byte pieces of 32 rows each reach HBM as partial lines). A wave writes its
+    // 64 rows as FP16 when its largest |O^T / l| x vs_ref / 2^7 (an output magnitude) is at most
+    // kNarrowPartial, where FP16's relative 2^-12 keeps the error under 1e-3; otherwise as FP32
+    // (heavy-tailed V reaches |y| ~ 16: FP16 there is 4e-3 off, and no 16-bit format meets both
+    // the 2e-3 bar and the reference's per-element bound for every value of such a row). Each row
+    // has a 1 KB slot; FP16 rows fill its first half. Wave w stages rows (16-byte chunks
+    // XOR-swizzled by row) in a 32 KB region no other wave uses: K tiles, V tiles 0-1, V tiles
+    // 2-3, the Q^T chunks; FP32 rows in two passes of 32.
     static_assert(sizeof(kbuf) >= 32768 && 2 * sizeof(W64VTile) >= 32768 && sizeof(qlds) >= 32768,
-                  "an LDS region per wave holds its 64 FP16 rows");
+                  "an LDS region per wave holds 32 KB of rows");
     __syncthreads();   // every wave has read its last tile
     unsigned char *ostage = wave == 0   ? reinterpret_cast<unsigned char *>(kbuf)
                             : wave == 1 ? reinterpret_cast<unsigned char *>(&vbuf[0])
@@ -913,41 +943,81 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
                                         : reinterpret_cast<unsigned char *>(qlds);
     unsigned char *pbase = reinterpret_cast<unsigned char *>(p.partial) +
                            (((size_t)g * p.tiles + tile) * p.splits + split) * kPartialBytes;
+    // FP16 rows are staged first, the wave's largest magnitude taken on the way; a wave whose
+    // outputs are too large then stages its rows again as FP32 from the accumulators
     typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+    float inv_l[2], zmax = 0.0f;
 #pragma unroll
     for (int rb = 0; rb < 2; rb++) {
         const int row = 32 * rb + i;   // of the wave's 64
-        const float inv_l = l[rb] > 0.0f ? 1.0f / l[rb] : 0.0f;
+        inv_l[rb] = l[rb] > 0.0f ? 1.0f / l[rb] : 0.0f;
 #pragma unroll
         for (int dt = 0; dt < 8; dt++)
 #pragma unroll
             for (int vq = 0; vq < 4; vq++) {
                 const int chunk = 4 * dt + vq;   // dimensions 8 chunk .. 8 chunk + 7; this lane's half at 4 kk
-                const half4 hv = {(_Float16)(o[rb][dt][4 * vq] * inv_l), (_Float16)(o[rb][dt][4 * vq + 1] * inv_l),
-                                  (_Float16)(o[rb][dt][4 * vq + 2] * inv_l), (_Float16)(o[rb][dt][4 * vq + 3] * inv_l)};
+                const float z0 = o[rb][dt][4 * vq] * inv_l[rb], z1 = o[rb][dt][4 * vq + 1] * inv_l[rb];
+                const float z2 = o[rb][dt][4 * vq + 2] * inv_l[rb], z3 = o[rb][dt][4 * vq + 3] * inv_l[rb];
+                zmax = max3f(zmax, max3f(fabsf(z0), fabsf(z1), fabsf(z2)), fabsf(z3));
+                const half4 hv = {(_Float16)z0, (_Float16)z1, (_Float16)z2, (_Float16)z3};
                 *reinterpret_cast<half4 *>(ostage + row * 512 + ((chunk ^ (row & 31)) * 16) + 8 * kk) = hv;
             }
-        if (kk == 0) {
-            const int local_row = 64 * wave + row;
-            float *stat = reinterpret_cast<float *>(pbase + (size_t)kTileRows * 256 * 2);
+    }
+#pragma unroll
+    for (int o2 = 32; o2 > 0; o2 >>= 1) zmax = fmaxf(zmax, __shfl_xor(zmax, o2, 64));
+    const bool wide = __builtin_amdgcn_readfirstlane(zmax * vs_out > kNarrowPartial ? 1u : 0u) != 0u;
+    if (kk == 0) {
+#pragma unroll
+        for (int rb = 0; rb < 2; rb++) {
+            const int local_row = 64 * wave + 32 * rb + i;
+            float *stat = reinterpret_cast<float *>(pbase + 2 * kPartialRegion);
             stat[local_row] = m[rb];
             stat[kTileRows + local_row] = l[rb];
-            stat[2 * kTileRows + local_row] = vs_ref;
+            stat[2 * kTileRows + local_row] = wide ? -vs_out : vs_out;   // the sign carries the format
         }
     }
     unsigned char *pw = pbase + (size_t)(64 * wave) * 512;   // the wave's rows are contiguous
+    if (!wide) {
 #pragma unroll
-    for (int it = 0; it < 32; it++) {
-        const int row = 2 * it + (lane >> 5), chunk = lane & 31;
-        const uint4 v = *reinterpret_cast<const uint4 *>(ostage + row * 512 + ((chunk ^ (row & 31)) * 16));
-        *reinterpret_cast<uint4 *>(pw + (size_t)it * 1024 + lane * 16) = v;
+        for (int it = 0; it < 32; it++) {
+            const int row = 2 * it + (lane >> 5), chunk = lane & 31;
+            const uint4 v = *reinterpret_cast<const uint4 *>(ostage + row * 512 + ((chunk ^ (row & 31)) * 16));
+            *reinterpret_cast<uint4 *>(pw + (size_t)it * 1024 + lane * 16) = v;
+        }
+        return;
+    }
+    // (the accumulators are read by explicit moves, so that the compiler holds no vector-register
+    // copies of them from the FP16 staging across the branch)
+    auto acc_read = [&](const float &a) __attribute__((always_inline)) {
+        float t;
+        asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(t) : "a"(a));
+        return t;
+    };
+#pragma unroll
+    for (int rb = 0; rb < 2; rb++) {
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++)
+#pragma unroll
+            for (int vq = 0; vq < 4; vq++) {
+                const int chunk = 8 * dt + 2 * vq + kk;   // dimensions 4 chunk .. 4 chunk + 3
+                const float4 fv = make_float4(
+                    acc_read(o[rb][dt][4 * vq]) * inv_l[rb], acc_read(o[rb][dt][4 * vq + 1]) * inv_l[rb],
+                    acc_read(o[rb][dt][4 * vq + 2]) * inv_l[rb], acc_read(o[rb][dt][4 * vq + 3]) * inv_l[rb]);
+                *reinterpret_cast<float4 *>(ostage + i * 1024 + ((chunk ^ i) * 16)) = fv;
+            }
+#pragma unroll
+        for (int r = 0; r < 32; r++) {   // lanes 0-31: dimensions 0-127 to region A, lanes 32-63 to B
+            const uint4 v = *reinterpret_cast<const uint4 *>(ostage + r * 1024 + ((lane ^ r) * 16));
+            *reinterpret_cast<uint4 *>(pw + (lane >> 5) * kPartialRegion + (size_t)(32 * rb + r) * 512 + (lane & 31) * 16) = v;
+        }
     }
 }
 
-// Merges the FP16 split partials of prefill_w64_kernel (O^T / l, then m, l, vs_ref per
-// row): one wave per logical row, four dimensions per lane, eight splits per step with
-// a running maximum, as prefill_combine_kernel.
-__global__ __launch_bounds__(256) void prefill_combine_half_kernel(PrefillParams p) {
+// Merges the split partials of prefill_w64_kernel (O^T / l, FP16 or FP32 per the row's format,
+// then m, l, +-vs_ref / 2^7): one wave per logical row, four dimensions per lane, eight splits per
+// step with a running maximum. The FP16 loads go out with the statistics; a split whose rows are
+// FP32 is read again in full once its format is known.
+__global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillParams p) {
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t local_row = blockIdx.x * 4 + (threadIdx.x >> 6), tile = blockIdx.y, g = blockIdx.z;
     const uint32_t row = tile * kTileRows + local_row;
@@ -962,16 +1032,32 @@ __global__ __launch_bounds__(256) void prefill_combine_half_kernel(PrefillParams
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (uint32_t s0 = 0; s0 < p.splits; s0 += 8) {
         float ms[8], ls[8], ws[8];
-        half4 os[8];
+        half4 hs[8];
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const uint32_t s = min(s0 + j, p.splits - 1);
             const unsigned char *part = base + s * kPartialBytes;
-            const float *stat = reinterpret_cast<const float *>(part + (size_t)kTileRows * 256 * 2);
+            const float *stat = reinterpret_cast<const float *>(part + 2 * kPartialRegion);
             ms[j] = s0 + j < p.splits ? stat[local_row] : -INFINITY;
             ls[j] = stat[kTileRows + local_row];
             ws[j] = stat[2 * kTileRows + local_row];
-            os[j] = *reinterpret_cast<const half4 *>(reinterpret_cast<const _Float16 *>(part) + (size_t)local_row * 256 + 4 * lane);
+            hs[j] = *reinterpret_cast<const half4 *>(part + (size_t)local_row * 512 + 8 * lane);
+        }
+        float4 os[8];
+        bool wide = false;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            os[j] = make_float4((float)hs[j].x, (float)hs[j].y, (float)hs[j].z, (float)hs[j].w);
+            wide |= ws[j] < 0.0f;
+        }
+        if (wide) {   // wave-uniform and rare: some split's rows are FP32
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                if (ws[j] < 0.0f) {
+                    const uint32_t s = min(s0 + j, p.splits - 1);
+                    os[j] = *reinterpret_cast<const float4 *>(base + s * kPartialBytes + (lane >> 5) * kPartialRegion +
+                                                              (size_t)local_row * 512 + 16 * (lane & 31));
+                }
         }
         float mstep = ms[0];
 #pragma unroll
@@ -990,12 +1076,12 @@ __global__ __launch_bounds__(256) void prefill_combine_half_kernel(PrefillParams
             if (ms[j] == -INFINITY) continue;
             const float f = __builtin_amdgcn_exp2f(ms[j] - mnew);
             const float lf = ls[j] * f;
-            const float wf = lf * ws[j];
+            const float wf = lf * fabsf(ws[j]);
             lsum += lf;
-            acc.x += (float)os[j].x * wf;
-            acc.y += (float)os[j].y * wf;
-            acc.z += (float)os[j].z * wf;
-            acc.w += (float)os[j].w * wf;
+            acc.x += os[j].x * wf;
+            acc.y += os[j].y * wf;
+            acc.z += os[j].z * wf;
+            acc.w += os[j].w * wf;
         }
     }
     const float inv = 1.0f / lsum;
@@ -1071,7 +1157,7 @@ const char *launch_prefill(Context &c, const View *b, const boot_kernel_args &a,
         launch_timed(c, "prefill_w64_fp16_kernel", prefill_w64_kernel<false>, dim3((uint32_t)blocks), dim3(256), p);
     if (splits > 1) {
         context_split(c, int8 ? "attention_online_int8.combine" : "attention_online_fp16.combine");
-        launch_timed(c, "prefill_combine_half_kernel", prefill_combine_half_kernel, dim3(kTileRows / 4, p.tiles, 2), dim3(256), p);
+        launch_timed(c, "prefill_combine_kernel", prefill_combine_kernel, dim3(kTileRows / 4, p.tiles, 2), dim3(256), p);
     }
     return nullptr;
 }

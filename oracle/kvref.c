@@ -308,7 +308,10 @@ static float sigmoid_f32(float g) {
  * summation order is not observable here); exp is the C library's expf.
  * p_mode 1 replaces (:1427) by this build's rounding, FP16(e * (vs / vs_ref)) with vs_ref the
  * largest V scale over the attended keys, and multiplies vs_ref back at the end;
- * p_mode 2 keeps P = e * vs in FP32 (no operand rounding). */
+ * p_mode 2 keeps P = e * vs in FP32 (no operand rounding);
+ * p_mode 3 is this build's current form: P = FP16(e * r) with r = 2^7 vs / vs_ref (2^7 for a
+ * zero V vector), the denominator sums P * (1 / r) (the rounded operand divided back by its
+ * factor) instead of e, and vs_ref / 2^7 multiplies the result at the end. */
 static void online_one(online_job *j, int row, int head, float *vals) {
     const int g = head / 8, length = j->pos + row + 1, T = j->tile_keys;
     float q[256];
@@ -354,6 +357,14 @@ static void online_one(online_job *j, int row, int head, float *vals) {
                 volatile float ratio = vsc * vs_inv;
                 volatile float scaled = value * ratio;
                 p = kvref_half_to_float(kvref_half_bits(scaled));
+            } else if (j->p_mode == 3) {
+                volatile float ratio = vsc * vs_inv;
+                volatile float r = vsc > 0.0f ? ratio * 128.0f : 128.0f;
+                volatile float scaled = value * r;
+                volatile float inverse = 1.0f / r;
+                p = kvref_half_to_float(kvref_half_bits(scaled));
+                volatile float weight = p * inverse;
+                value = weight;   /* the denominator takes the rounded operand, divided back */
             } else {
                 volatile float scaled = value * vsc;
                 p = scaled;
@@ -373,7 +384,7 @@ static void online_one(online_job *j, int row, int head, float *vals) {
     }
     float *y = j->out + ((size_t)row * 16 + head) * 256;
     for (int d = 0; d < 256; d++) {
-        volatile float o = j->p_mode == 1 ? out[d] * vs_ref : out[d];
+        volatile float o = j->p_mode == 1 ? out[d] * vs_ref : j->p_mode == 3 ? out[d] * (vs_ref / 128.0f) : out[d];
         volatile float r = o / denominator;
         y[d] = r * sigmoid_f32(j->gate[((size_t)row * 16 + head) * 256 + d]);
     }

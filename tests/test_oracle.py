@@ -337,14 +337,16 @@ def test_online_emulator_unrounded_equals_fp64(oracle, history, rows, tile):
 
 def test_online_emulator_one_key_exact(oracle):
     """One key: P = round(e * vs) with e = 1 (kernels.metal:1426-1427), so y is the rounded V
-    scale (BF16 in the reference, 1 * vs_ref in this build's FP16 form) times the code times
-    sigmoid(gate)."""
+    scale (BF16 in the reference, 1 * vs_ref in this build's FP16 forms) times the code times
+    sigmoid(gate); with the denominator summing the rounded operand (mode 3) the key's value
+    comes back exactly."""
     import torch
     q, gate, (kc, vc, ks, vs) = emulator_case(oracle, 0, 1)
     codes = np.array([[vc[oracle.value_index(g, d)] for d in range(256)] for g in range(2)], np.float64)
     sig = 1 / (1 + np.exp(-gate.reshape(16, 256).astype(np.float64)))
     bf = torch.from_numpy(vs[:2].copy()).to(torch.bfloat16).to(torch.float32).numpy().astype(np.float64)
-    for mode, scale in ((0, bf), (1, vs[:2].astype(np.float64)), (2, vs[:2].astype(np.float64))):
+    for mode, scale in ((0, bf), (1, vs[:2].astype(np.float64)), (2, vs[:2].astype(np.float64)),
+                        (3, vs[:2].astype(np.float64))):
         y = oracle.online_emulate(q, kc, vc, ks, vs, gate, 1, 0, p_mode=mode).reshape(16, 256)
         for h in range(16):
             want = codes[h // 8] * scale[h // 8] * sig[h]
@@ -358,15 +360,42 @@ def test_probability_operand_rounding_against_the_bar(oracle, history, rows):
     bfloat(e * vs) (kernels.metal:1427): on the reference's own test distribution
     (Int8KvTests.cs:107-113) the BF16 operand alone moves the output rel-L2 1.6e-3..3.2e-3
     from FP64 - outside the rel-L2 1e-3 bar, though inside the reference's per-element bound
-    sum|p v| / 256 + 1e-4 (Int8KvTests.cs:154-156) - while the FP16 operand stays near 1.5e-4."""
+    sum|p v| / 256 + 1e-4 (Int8KvTests.cs:154-156) - while the FP16 operand stays near 1.5e-4,
+    in both its first form (mode 1) and the current one (mode 3: 2^7-scaled, the denominator
+    summing the rounded operands)."""
     from kvcase import rel_l2
     q, gate, cache = emulator_case(oracle, history, rows)
     ref, bound = oracle.attention(q, *cache, gate, rows, history, round_q_half=1, with_bound=True)
     bf16 = oracle.online_emulate(q, *cache, gate, rows, history, p_mode=0)
-    fp16 = oracle.online_emulate(q, *cache, gate, rows, history, p_mode=1)
     assert rel_l2(bf16, ref) > 1.5e-3
     assert np.all(np.abs(bf16 - ref) <= bound / 256 + 1e-4)
-    assert rel_l2(fp16, ref) < 2.5e-4 and np.abs(fp16 - ref).max() < 2e-4
+    for mode in (1, 3):
+        fp16 = oracle.online_emulate(q, *cache, gate, rows, history, p_mode=mode)
+        assert rel_l2(fp16, ref) < 2.5e-4 and np.abs(fp16 - ref).max() < 2e-4, mode
+
+
+@pytest.mark.parametrize("seed", [600, 630])
+def test_probability_denominator_on_heavy_tailed_values(oracle, seed):
+    """Student-t (nu = 4) K and V (config 5's distribution) give rows dominated by a few keys with
+    large values (|y| ~ 5 here, ~16 at longer histories). With the denominator summing the
+    unrounded e (mode 1) the operand's relative rounding returns as an absolute error that grows
+    with |y|; summing the rounded operands divided back by their factor (mode 3, the kernel's
+    form) moves numerator and denominator together: at most half mode 1's largest error, and a
+    lower rel-L2."""
+    from kvcase import rel_l2
+    history, rows = 4096, 64
+    length = history + rows
+    k = oracle.student_t4(length * 512, seed).reshape(length, 2, 256)
+    v = oracle.student_t4(length * 512, seed + 1).reshape(length, 2, 256)
+    cache = oracle.empty_cache(length)
+    oracle.store_mt(k, v, 0, *cache)
+    q, gate = oracle.normal(rows * 4096, seed + 2), oracle.normal(rows * 4096, seed + 3)
+    ref = oracle.attention(q, *cache, gate, rows, history, round_q_half=1)
+    first = oracle.online_emulate(q, *cache, gate, rows, history, p_mode=1).astype(np.float64)
+    current = oracle.online_emulate(q, *cache, gate, rows, history, p_mode=3).astype(np.float64)
+    assert np.abs(ref).max() > 4
+    assert np.abs(current - ref).max() <= 0.5 * np.abs(first - ref).max()
+    assert rel_l2(current, ref) < rel_l2(first, ref) and np.abs(current - ref).max() < 2e-3
 
 
 def test_threaded_store_writes_the_same_bytes(oracle):
