@@ -98,16 +98,20 @@ int boot_write(void *ctx, void *buf, uint64_t offset, const void *host, uint64_t
 int boot_read(void *ctx, void *buf, uint64_t offset, void *host, uint64_t bytes);
 
 /* ---- No counterpart in the reference. For callers that cannot allocate device memory
- * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). ----
+ * (tight serving loops, harnesses that forbid hipMalloc). ----
  *
  * boot_dispatch with the same arguments and outputs, except that kernels whose launch needs
- * split-K scratch (attention_decode_int8, the attention_online_* prefill names) draw it from a
- * static 48 MiB device array of the library instead of the context workspace; it calls no
- * hipMalloc/hipFree or other allocating routine and records no timing sample. Requests larger
- * than 48 MiB are rejected (0, with the size in boot_error) before any launch; 48 MiB covers
- * every prefill chunk on 256 CUs and single-token decode up to the 262144 window. Every call on
- * one GPU shares that GPU's array: calls that overlap on one GPU (other contexts or threads)
- * race; calls in one context's command are ordered on its stream. */
+ * split-K scratch (attention_decode_int8, attention_decode_append_int8, the attention_online_*
+ * prefill names) draw it from a static 72 MiB device array of the library instead of the context
+ * workspace; it calls no hipMalloc/hipFree or other allocating routine and records no timing
+ * sample. Requests larger than 72 MiB are rejected (0, with the size in boot_error) before any
+ * launch; 72 MiB covers prefill chunks of up to 512 rows and of 2048 rows on 256 CUs, and
+ * single-token decode up to the 262144 window. One GPU has one array: the first split-K call of a command claims it
+ * for that context until the command's boot_end, and a split-K call of another context meanwhile
+ * fails (0, "held by another context's command") instead of racing; calls in one context's
+ * command are ordered on its stream. The context's stream is the library's own and boot_end
+ * synchronizes it, so this entry point does not make the library's work capturable into a HIP
+ * graph. */
 int boot_dispatch_noalloc(void *ctx, const char *name, void **buffers, const uint64_t *offsets, int count,
                           const void *params, int param_bytes, uint32_t x, uint32_t y, uint32_t z,
                           uint32_t tx, uint32_t ty, uint32_t tz, void *indirect, uint64_t indirect_offset);

@@ -11,6 +11,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <chrono>
 #include <map>
 #include <mutex>
@@ -23,11 +24,12 @@
 
 namespace boot {
 
-// Split-K scratch of boot_dispatch_noalloc (the attention kernels' per-split partials): 48 MiB,
-// enough for every prefill chunk on 256 CUs (one partial of at most 134,144 bytes per CU) and
-// for single-token decode up to the 262144 window (about 2 MiB). Each device holds its own copy
-// until the process ends; the host reaches it only through the address kept per device below.
-constexpr uint64_t kStaticScratchBytes = 48ull << 20;
+// Split-K scratch of boot_dispatch_noalloc (the attention kernels' per-split partials): 72 MiB,
+// enough for prefill chunks of up to 512 rows and of 2048 rows on 256 CUs (at most 279 partials
+// of 265,216 bytes) and for single-token decode up to the 262144 window (about 2 MiB). Each
+// device holds its own copy until the process ends; the host reaches it only through the
+// address kept per device below.
+constexpr uint64_t kStaticScratchBytes = 72ull << 20;
 
 }  // namespace boot
 
@@ -40,6 +42,10 @@ constexpr int kMaxDevices = 64;
 std::once_flag scratch_once[kMaxDevices];
 void *scratch_address[kMaxDevices];
 hipError_t scratch_status[kMaxDevices];
+// The context whose open command holds the device's scratch (from its first split-K
+// boot_dispatch_noalloc until its boot_end), or null: a noalloc split-K dispatch of any other
+// context meanwhile is refused instead of racing on the partials.
+std::atomic<const void *> scratch_owner[kMaxDevices];
 
 // Device address of `scratch` on the current device, looked up once per device (the array's
 // name is a host-side stand-in, never a device address). Null with the HIP error if the lookup
@@ -87,6 +93,7 @@ struct Context {
     void *scratch = nullptr;
     hipError_t scratch_status = hipSuccess;
     uint64_t scratch_request = 0;   // bytes the last refused request asked for
+    bool scratch_busy = false;      // the last request found the scratch held by another context
     // serialized per-dispatch profiling (bridge.mm:61,198-204)
     bool profile = false;
     std::map<std::string, std::pair<double, uint64_t>> timings;
@@ -191,6 +198,11 @@ void *context_workspace(Context &c, uint64_t bytes) {
             c.scratch_request = bytes;
             return nullptr;
         }
+        const void *expected = nullptr;
+        if (!scratch_owner[c.device].compare_exchange_strong(expected, &c) && expected != &c) {
+            c.scratch_busy = true;
+            return nullptr;
+        }
         return c.scratch;
     }
     if (bytes <= c.workspace_bytes) return c.workspace;
@@ -231,6 +243,13 @@ void context_split(Context &c, const char *name) {
     c.current_name = name;
     c.current_start = e;
     c.current_kind = -1;
+}
+
+// Gives the device's scratch back if this context's command held it; called once the context's
+// stream has drained (its kernels no longer read or write the scratch).
+void release_scratch(Context &c) {
+    const void *self = &c;
+    scratch_owner[c.device].compare_exchange_strong(self, nullptr);
 }
 
 }  // namespace boot
@@ -312,6 +331,7 @@ void boot_destroy(void *handle) {
     if (!c) return;
     // teardown: an error here has no caller left to reach, so each call is best effort
     (void)hipStreamSynchronize(c->stream);
+    release_scratch(*c);
     if (c->profile)
         for (auto &entry : c->timings)
             fprintf(stderr, "GPU_DIAGNOSTIC %s count=%llu gpu_ms=%.6f\n", entry.first.c_str(),
@@ -478,6 +498,11 @@ int dispatch(Context *c, const char *name, void **buffers, const uint64_t *offse
         c->samples.push_back({c->current_name, c->current_start, e, c->current_kind});
         c->sampling = false;
     }
+    if (message && noalloc && c->scratch_busy) {
+        c->scratch_busy = false;
+        return fail(c, std::string(name) + ": the static scratch of boot_dispatch_noalloc is held by another "
+                                           "context's command until its boot_end");
+    }
     if (message && noalloc && c->scratch_request > kStaticScratchBytes) {
         const uint64_t asked = c->scratch_request;
         c->scratch_request = 0;
@@ -529,6 +554,7 @@ int boot_end(void *handle) {
     if (c->wall_enabled) c->command_end = record(c);
     hipError_t e = hipStreamSynchronize(c->stream);
     c->active = false;
+    if (e == hipSuccess) release_scratch(*c);
     if (e != hipSuccess) return hip_ok(c, e, "command failed");
     if (c->wall_enabled) {
         double done = wall_now();

@@ -1,10 +1,13 @@
 """boot_dispatch_noalloc (the entry point that allocates nothing) against boot_dispatch on the
-same inputs: split-K decode and prefill, two calls in a row with the second smaller, results
-bitwise equal and within the FP64 bar; sizes beyond the static scratch are refused."""
+same inputs: split-K decode and prefill on a fresh context, the no-allocation calls first (before
+the context has any workspace) with boot_allocated unchanged across each of them, two calls in a
+row with the second smaller, results bitwise equal and within the FP64 bar; sizes beyond the
+static scratch are refused, and so is a second context's split-K call while the first context's
+command holds the scratch."""
 import numpy as np
 import pytest
 
-from bootstrap_hip import HipError, KernelArgs
+from bootstrap_hip import Device, HipError, KernelArgs
 from kvcase import outlier_kv, poison_tail, reference_kv, rel_l2, upload, upload_cache
 
 pytestmark = pytest.mark.gpu
@@ -21,10 +24,13 @@ def decode(device, q, gate, cache, rows, history, noalloc):
     qb, gb = upload(device, q), upload(device, gate)
     out = device.allocate(q.nbytes + 4)
     out.write(np.full(rows * 4096 + 1, np.nan, np.float32))
+    before = device.allocated_bytes
     device.begin()
     device.dispatch("attention_decode_int8", KernelArgs(M=rows, K=history + rows, Position=history), rows * 4096, 256,
                     qb, cache.kc, cache.vc, gb, out, cache.ks, cache.vs, noalloc=noalloc)
     device.end()
+    if noalloc:
+        assert device.allocated_bytes == before, "boot_dispatch_noalloc allocated device memory"
     y = out.read(np.float32, rows * 4096 + 1)
     for b in (qb, gb, out):
         b.dispose()
@@ -37,11 +43,14 @@ def prefill(device, q, gate, cache, rows, history, noalloc):
     packed, out = device.allocate(rows * 8192), device.allocate(q.nbytes + 4)
     out.write(np.full(rows * 4096 + 1, np.nan, np.float32))
     p = KernelArgs(M=rows, K=history + rows, Position=history, A=8)
+    before = device.allocated_bytes
     device.begin()
     device.dispatch("attention_query_grouped_half", p, rows * 1024, 128, qb, packed, noalloc=noalloc)
     device.dispatch2d("attention_online_int8_q32_k256_r2", p, (rows * 8 + 31) // 32 * 256, 2, 256, packed, cache.kc,
                       cache.vc, gb, out, cache.ks, cache.vs, noalloc=noalloc)
     device.end()
+    if noalloc:
+        assert device.allocated_bytes == before, "boot_dispatch_noalloc allocated device memory"
     y = out.read(np.float32, rows * 4096 + 1)
     for b in (qb, gb, packed, out):
         b.dispose()
@@ -51,23 +60,62 @@ def prefill(device, q, gate, cache, rows, history, noalloc):
 
 @pytest.mark.parametrize("kind,cases", [
     ("decode", [(131071, 1), (4093, 7)]),        # 114 splits per group, then 6
-    ("prefill", [(30208, 512), (257, 33)]),      # 34.3 MB of partials, then 8 splits of one tile
+    ("prefill", [(30208, 512), (257, 33)]),      # 68 MB of partial slots, then 8 splits of one tile
 ])
-def test_noalloc_matches_dispatch(device, oracle, kind, cases):
+def test_noalloc_matches_dispatch(oracle, kind, cases):
+    """A fresh context: every no-allocation call runs before the context has a workspace, so a
+    path that fell back to (or grew) the workspace would show in boot_allocated."""
     run = decode if kind == "decode" else prefill
-    for history, rows in cases:
-        length = history + rows
-        kv = outlier_kv(oracle, length, seed=70) if length > 100000 else reference_kv(length)
-        host = host_cache(oracle, length, kv)
-        cache = upload_cache(device, *host)
-        q = oracle.fill_hash(rows * 4096, 17, 3)
-        gate = oracle.fill_hash(rows * 4096, 11, 1)
-        expected = run(device, q, gate, cache, rows, history, noalloc=False)
-        got = run(device, q, gate, cache, rows, history, noalloc=True)
-        assert np.array_equal(got.view(np.uint32), expected.view(np.uint32)), (kind, history, rows)
-        ref = oracle.attention(q, *host, gate, rows, history, round_q_half=1 if kind == "prefill" else 0)
-        assert rel_l2(got, ref) <= 1e-3 and np.abs(got - ref).max() <= 2e-3
-        cache.dispose()
+    with Device() as device:
+        prepared = []
+        for history, rows in cases:
+            length = history + rows
+            kv = outlier_kv(oracle, length, seed=70) if length > 100000 else reference_kv(length)
+            host = host_cache(oracle, length, kv)
+            q = oracle.fill_hash(rows * 4096, 17, 3)
+            gate = oracle.fill_hash(rows * 4096, 11, 1)
+            prepared.append((history, rows, host, upload_cache(device, *host), q, gate))
+        got = [run(device, q, gate, cache, rows, history, noalloc=True) for history, rows, _, cache, q, gate in prepared]
+        for (history, rows, host, cache, q, gate), y in zip(prepared, got):
+            expected = run(device, q, gate, cache, rows, history, noalloc=False)
+            assert np.array_equal(y.view(np.uint32), expected.view(np.uint32)), (kind, history, rows)
+            ref = oracle.attention(q, *host, gate, rows, history, round_q_half=1 if kind == "prefill" else 0)
+            assert rel_l2(y, ref) <= 1e-3 and np.abs(y - ref).max() <= 2e-3
+            cache.dispose()
+
+
+def test_noalloc_scratch_held_by_one_context_command(device, oracle):
+    """While one context's command holds the device's scratch (after its first split-K
+    no-allocation call, until its boot_end), a split-K no-allocation call of another context is
+    refused on the host before any launch; after boot_end it runs and matches."""
+    history, rows = 4093, 7
+    host = host_cache(oracle, history + rows, reference_kv(history + rows))
+    q = oracle.fill_hash(rows * 4096, 17, 3)
+    gate = oracle.fill_hash(rows * 4096, 11, 1)
+    cache = upload_cache(device, *host)
+    qb, gb, out = upload(device, q), upload(device, gate), device.allocate(q.nbytes)
+    p = KernelArgs(M=rows, K=history + rows, Position=history)
+    with Device() as other:
+        ocache = upload_cache(other, *host)
+        oq, og, oout = upload(other, q), upload(other, gate), other.allocate(q.nbytes)
+        device.begin()
+        device.dispatch("attention_decode_int8", p, rows * 4096, 256, qb, cache.kc, cache.vc, gb, out, cache.ks,
+                        cache.vs, noalloc=True)
+        other.begin()
+        with pytest.raises(HipError, match="held by another context"):
+            other.dispatch("attention_decode_int8", p, rows * 4096, 256, oq, ocache.kc, ocache.vc, og, oout, ocache.ks,
+                           ocache.vs, noalloc=True)
+        other.end()
+        device.end()
+        other.begin()
+        other.dispatch("attention_decode_int8", p, rows * 4096, 256, oq, ocache.kc, ocache.vc, og, oout, ocache.ks,
+                       ocache.vs, noalloc=True)
+        other.end()
+        a, b = out.read(np.float32, rows * 4096), oout.read(np.float32, rows * 4096)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    for buf in (qb, gb, out):
+        buf.dispose()
+    cache.dispose()
 
 
 def test_noalloc_refuses_beyond_the_static_scratch(device, oracle):
