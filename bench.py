@@ -143,6 +143,53 @@ class PrefillWorkload:
         return sum(prefill_flops(pos, min(self.chunk, self.tokens - pos)) for pos in range(0, self.tokens, self.chunk))
 
 
+# (history, query rows, the reference's GPU median in ms on an M5 Pro) of its INT8 online kernel
+# (docs/INT8_30K_PREFILL_20261104.md:59-61)
+REFERENCE_SHAPES = [(0, 33, 0.02408), (8192, 2048, 14.82842), (27900, 2048, 44.22633)]
+
+
+def reference_shapes(work: PrefillWorkload, runs: int = 20):
+    """attention_online_int8_q32_k256_r2 at the shapes the reference times it at, over config 3's
+    cache: the query and gate prepared by attention_prepare_fused_int8 at those rows (which rewrites
+    the same cache rows with the same bytes), then `runs` launches timed kernel-exact (attention
+    kernel + split combine, averaged). The M5 Pro medians are context, not a same-node comparison."""
+    d = work.device
+    ws = engine.DeviceAttentionWorkspace(d)
+    ws.prepare(2048)
+    gate, out = d.allocate(2048 * 16384), d.allocate(2048 * 16384)
+    layer = work.layer
+    entries = []
+    for history, rows, m5 in REFERENCE_SHAPES:
+        d.begin()
+        engine.prepare_fused(d, layer, work.qkv.at(history * 32768), work.k.at(history * 2048), work.v.at(history * 2048),
+                             work.q_norm, work.k_norm, ws.packed_query, gate, rows, history)
+        for _ in range(3):
+            ws.encode_int8(None, layer.key, layer.value, layer.key_scale, layer.value_scale, gate, out, rows, history,
+                           prepared_query=True)
+        d.end()
+        d.reset_wall_timing(kernels_exact=True)
+        d.begin()
+        for _ in range(runs):
+            ws.encode_int8(None, layer.key, layer.value, layer.key_scale, layer.value_scale, gate, out, rows, history,
+                           prepared_query=True)
+        d.end()
+        ks = kernel_stats(d, ["prefill_w64_kernel", "prefill_combine_kernel"])
+        attn = ks["prefill_w64_kernel"][0] / runs
+        comb = ks.get("prefill_combine_kernel", (0.0, 0))[0] / runs
+        flops = prefill_flops(history, rows)
+        entries.append({"history": history, "rows": rows, "attention_kernel_ms": round(attn, 5),
+                        "combine_ms": round(comb, 5), "ms": round(attn + comb, 5),
+                        "mfma_frac_attention_kernel": round(flops / (attn * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
+                        "reference_m5pro_gpu_median_ms": m5})
+    for b in (gate, out):
+        b.dispose()
+    ws.dispose()
+    return {"what": "attention_online_int8_q32_k256_r2 at the reference's timed shapes (history, query rows), "
+                    f"kernel-exact, mean of {runs} launches over config 3's cache; the reference's figures are GPU "
+                    "medians on an Apple M5 Pro (docs/INT8_30K_PREFILL_20261104.md:59-61), context only",
+            "shapes": entries}
+
+
 class Fp16ControlWorkload:
     """The same prompt with FP16 KV storage (config 3's side-by-side comparator), in the same
     shape: attention_prepare_fused (FP16 K/V) -> attention_online_q32_k256_s8_g8_r2 on the
@@ -199,13 +246,16 @@ def _rotated_queries(q_host, pos):
     return np.ascontiguousarray(q.astype(np.float32).ravel())
 
 
-def cpu_baseline(work: "PrefillWorkload", dec: "DecodeWorkload", runs: int = 5):
+def cpu_baseline(work: "PrefillWorkload", dec: "DecodeWorkload", y_last, runs: int = 5):
     """The reference's scalar CPU checker restated in C (the oracle: FP64 attention of
     Int8KvTests.cs:130-158 over the INT8 cache, append of Int8KvTests.cs:116-118), work split over
     (row, head) for attention and over tokens for append, on the host threads; median of `runs`
     runs of each workload on the same seeded inputs as the GPU path. ``value`` is config 3 in
     ms/layer: its last 512-query chunk timed in full and scaled by the causal flop ratio to the
-    whole 30720-token layer (labelled as extrapolated)."""
+    whole 30720-token layer (labelled as extrapolated). Also the parity check of what was timed:
+    ``y_last`` (the INT8 path's output of the last chunk) against the same FP64 attention, with the
+    bar rel-L2 <= 1e-3, max-abs <= 2e-3 and the per-element bound of Int8KvTests.cs:154-156, and
+    the finished cache's V codes and scales against the oracle's quantizer."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from oracle_lib import Oracle
     threads, nproc, affinity = host_threads()
@@ -268,6 +318,20 @@ def cpu_baseline(work: "PrefillWorkload", dec: "DecodeWorkload", runs: int = 5):
     g3 = work.gate.read(np.float32, chunk * 4096)
     last = _spread(_timed(lambda: oracle.attention(q3, *cache3, g3, chunk, pos, round_q_half=1), runs))
     ratio = work.flops() / prefill_flops(pos, chunk)
+    # parity of the timed chain (outside every timed region): the last chunk's output and the V cache
+    ref, bound = oracle.attention(q3, *cache3, g3, chunk, pos, round_q_half=1, with_bound=True)
+    err = np.abs(y_last.astype(np.float64) - ref)
+    rel = float(np.linalg.norm(y_last.astype(np.float64) - ref) / np.linalg.norm(ref))
+    v_host = work.v.read(np.float32, tokens * 512).reshape(tokens, 2, 256)
+    okc, ovc, oks, ovs = oracle.empty_cache(tokens)
+    oracle.store_mt(np.zeros_like(v_host), v_host, 0, okc, ovc, oks, ovs)
+    v_equal = cache3[1].tobytes() == ovc.tobytes() and cache3[3].tobytes() == ovs.tobytes()
+    parity = {"what": f"INT8 output of the last timed chunk (queries {pos}-{tokens - 1}) vs FP64 attention over the "
+                      "device's cache and prepared FP16 query; V codes/scales of the 30720-token cache vs the oracle",
+              "rel_l2": float(f"{rel:.4g}"), "max_abs": float(f"{err.max():.4g}"),
+              "within_element_bound": bool(np.all(err <= bound / 256 + 1e-4)),
+              "v_cache_bitwise": bool(v_equal),
+              "pass": bool(rel <= 1e-3 and err.max() <= 2e-3 and np.all(err <= bound / 256 + 1e-4) and v_equal)}
     last["extrapolated_ms_per_layer"] = round(last["median_ms"] * ratio, 1)
     entries["config3_last_chunk"] = dict(last, what=f"queries {pos}-{tokens - 1} over {tokens} keys; x{ratio:.2f} causal flop ratio to the layer")
     return {"value": last["extrapolated_ms_per_layer"], "unit": "ms/layer", "cores": threads, "kind": "port",
@@ -276,7 +340,7 @@ def cpu_baseline(work: "PrefillWorkload", dec: "DecodeWorkload", runs: int = 5):
                       f"host threads (nproc {nproc}), median of {runs} runs per workload; value = config 3's last "
                       f"512-query chunk ({last['median_ms'] / 1000:.2f} s) extrapolated x{ratio:.1f} by the causal flop "
                       f"ratio to the 30720-token layer",
-            "entries": entries}
+            "entries": entries}, parity
 
 
 # --------------------------------------------------------------------------- decode
@@ -408,9 +472,10 @@ def main():
     attn_kernel = next((k for k in PREFILL_INT8_KERNELS if k in timed), None)
     if attn_kernel is None:
         raise SystemExit("no INT8 prefill attention kernel was timed")
-    ks = kernel_stats(device, [attn_kernel, "prefill_combine_half_kernel", "prepare_fused_int8_kernel"])
+    ks = kernel_stats(device, [attn_kernel, "prefill_combine_kernel", "prepare_fused_int8_kernel"])
+    y_int8 = work.out.read(np.float32, work.chunk * 4096)     # the last chunk's INT8 output
     attn_ms = ks[attn_kernel][0] / args.steps
-    combine_ms = ks.get("prefill_combine_half_kernel", (0.0, 0))[0] / args.steps
+    combine_ms = ks.get("prefill_combine_kernel", (0.0, 0))[0] / args.steps
     launches = ks[attn_kernel][1] // args.steps
     flops = work.flops()
     achieved = flops / (attn_ms * 1e-3) / 1e12
@@ -434,17 +499,26 @@ def main():
                      "counters": measured_counters(attn_kernel),
                      "flops_per_layer": flops},
     }
+    log("reference shapes: (0,33), (8192,2048), (27900,2048)")
+    result["reference_shapes"] = reference_shapes(work)
     device.reset_wall_timing(kernels_exact=True)
     for _ in range(args.steps):
         control.step()
-    kc = kernel_stats(device, ["prefill_w64_fp16_kernel", "prefill_combine_half_kernel", "prepare_fused_half_kernel"])
+    kc = kernel_stats(device, ["prefill_w64_fp16_kernel", "prefill_combine_kernel", "prepare_fused_half_kernel"])
+    y_fp16 = work.out.read(np.float32, work.chunk * 4096)     # the FP16-KV control's, same query and raw K/V
+    diff = y_int8.astype(np.float64) - y_fp16
     result["fp16_kv_control"] = {
         "ms_per_layer": round(fp16_ms, 4),
         "kernel": "prefill_w64_fp16_kernel (the INT8 kernel's schedule with FP16 staging)",
         "attention_kernel_ms_per_layer": round(kc.get("prefill_w64_fp16_kernel", (0.0, 0))[0] / args.steps, 4),
-        "combine_ms_per_layer": round(kc.get("prefill_combine_half_kernel", (0.0, 0))[0] / args.steps, 4),
+        "combine_ms_per_layer": round(kc.get("prefill_combine_kernel", (0.0, 0))[0] / args.steps, 4),
         "prepare_ms_per_layer": round(kc["prepare_fused_half_kernel"][0] / args.steps, 4),
         "int8_over_fp16_time": round(wall_ms / fp16_ms, 4),
+        "int8_vs_fp16_output": {"chunk": "last (queries 30208-30719)", "max_abs": float(f"{np.abs(diff).max():.4g}"),
+                                "rel_l2": float(f"{np.linalg.norm(diff) / np.linalg.norm(y_fp16):.4g}"),
+                                "what": "INT8-cache output minus FP16-cache output of the GPU paths (the quantization "
+                                        "error max_abs_quantization_vs_fp16 of Int8KvTests.cs:138-150, measured on "
+                                        "the kernels' outputs)"},
         "kv_bytes_30k": {"int8_with_scales": 30720 * 1040, "fp16": 30720 * 2048}}
     if dec is not None:
         device.reset_wall_timing(kernels_exact=True)
@@ -481,7 +555,7 @@ def main():
             "bytes": bulk_bytes, "kernel_ms": round(bulk, 4)}
     if not args.no_cpu_baseline:
         log("cpu baseline: the FP64 checker on configs 1, 2, a 131072 decode step and config 3's last chunk")
-        result["cpu_baseline"] = cpu_baseline(work, dec)
+        result["cpu_baseline"], result["parity_last_chunk"] = cpu_baseline(work, dec, y_int8)
     print(json.dumps(result), flush=True)
     device.close()
 

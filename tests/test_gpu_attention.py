@@ -45,10 +45,12 @@ def run_prefill(device, q, gate, cache, rows, history, alias=False, kernel="atte
     return y
 
 
-# the last two: config 3's final chunk at full size, and a block ending exactly at the
-# 262144-token window (ContextLimits.cs:5)
+# (30208, 512): config 3's final chunk at full size; (262080, 64): a block ending exactly at the
+# 262144-token window (ContextLimits.cs:5); (0, 33), (8192, 2048), (27900, 2048): the shapes the
+# reference times its INT8 online kernel at (docs/INT8_30K_PREFILL_20261104.md:59-61), 2048 rows
+# being the chunk its tuned preset dispatches (Program.cs:71, Prefill.cs:111-121)
 PREFILL_CASES = [(0, 1), (17, 7), (127, 31), (127, 32), (257, 33), (4093, 7), (8192, 128), (0, 512), (3584, 512),
-                 (30000, 33), (30208, 512), (262080, 64)]
+                 (30000, 33), (30208, 512), (262080, 64), (0, 33), (8192, 2048), (27900, 2048)]
 
 
 @pytest.mark.parametrize("history,rows", PREFILL_CASES)
