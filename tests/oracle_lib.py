@@ -9,7 +9,8 @@ import numpy as np
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 ORACLE_DIR = os.path.join(ROOT, "oracle")
-ORACLE_LIB = os.path.join(ORACLE_DIR, "libkvref.so")
+# KVREF_LIBRARY selects another build of the same source (the sanitizer build of `make sanitize`)
+ORACLE_LIB = os.environ.get("KVREF_LIBRARY", os.path.join(ORACLE_DIR, "libkvref.so"))
 
 _f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
 _f64p = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
