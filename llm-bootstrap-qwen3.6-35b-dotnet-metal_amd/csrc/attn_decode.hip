@@ -152,7 +152,11 @@ struct DecodeParams {
     float *ks_out, *vs_out;
 };
 
-__device__ inline float sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }
+// sigmoid(x) = 1 / (1 + 2^(-x log2(e))) with the hardware exponential and reciprocal (about an ulp
+// each), as the prefill kernels compute it
+__device__ inline float sigmoidf(float x) {
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
+}
 
 // x + x of lane l ^ 8 (the same position in the other half of its 16-lane row) for
 // the eight values of two accumulators: one DPP add each, as inline assembly (the DPP
@@ -688,12 +692,15 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
     float4 acc = make_float4(res[0] * vs_ref, res[1] * vs_ref, res[2] * vs_ref, res[3] * vs_ref);
     if (p.splits == 1) {
         // gate and y need only 4-byte alignment
+        // (the four gate loads go out before the first store: the compiler cannot tell y from gate)
         const size_t at = ((size_t)row * 16 + g * 8 + h) * 256 + d0;
         const float inv = 1.0f / lw;
-        p.y[at + 0] = acc.x * inv * sigmoidf(p.gate[at + 0]);
-        p.y[at + 1] = acc.y * inv * sigmoidf(p.gate[at + 1]);
-        p.y[at + 2] = acc.z * inv * sigmoidf(p.gate[at + 2]);
-        p.y[at + 3] = acc.w * inv * sigmoidf(p.gate[at + 3]);
+        const float g0 = p.gate[at + 0], g1 = p.gate[at + 1], g2 = p.gate[at + 2], g3 = p.gate[at + 3];
+        asm volatile("" ::"v"(g0), "v"(g1), "v"(g2), "v"(g3) : "memory");
+        p.y[at + 0] = acc.x * inv * sigmoidf(g0);
+        p.y[at + 1] = acc.y * inv * sigmoidf(g1);
+        p.y[at + 2] = acc.z * inv * sigmoidf(g2);
+        p.y[at + 3] = acc.w * inv * sigmoidf(g3);
         return;
     }
     float *part = p.partial + (((size_t)row * 2 + g) * p.splits + split) * kPartialFloats;

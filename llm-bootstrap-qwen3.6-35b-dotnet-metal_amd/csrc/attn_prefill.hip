@@ -75,7 +75,9 @@ struct PrefillParams {
     uint32_t remap;         // 1: XCD-aware block order
 };
 
-__device__ inline float sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }
+// sigmoid(x) = 1 / (1 + 2^(-x log2(e))) with the hardware exponential and reciprocal (about an ulp
+// each); a library expf and a correctly rounded division cost ~25 instructions per output element
+__device__ inline float sigmoidf(float x) { return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * kLog2e)); }
 
 // Key row of QK tile row i: bits 2 and 3 of i swapped (see header comment).
 __device__ inline int qk_key_row(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
@@ -903,23 +905,31 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
     // operands 2^7 e vs / vs_ref times the codes, so vs_ref / 2^7 turns O / l into values.
     const float vs_out = vs_ref * (1.0f / kPScale);
     if (p.splits == 1) {
+        // The row's 32 gate loads go out together before its first store: y may alias the query
+        // buffer, and the compiler, unable to tell y from the gate, would otherwise hold each load
+        // behind the previous store (one memory round trip per 16 bytes of output).
 #pragma unroll
         for (int rb = 0; rb < 2; rb++) {
-            if (!row_valid[rb]) continue;
             const uint32_t token = my_row[rb] / 8, head = g * 8 + my_row[rb] % 8;
             const size_t base = ((size_t)token * 16 + head) * 256;
             const float inv = vs_out / l[rb];
+            float4 gv[32];
+#pragma unroll
+            for (int c = 0; c < 32; c++)
+                gv[c] = row_valid[rb] ? *reinterpret_cast<const float4 *>(p.gate + base + 32 * (c >> 2) + 8 * (c & 3) + 4 * kk)
+                                      : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (!row_valid[rb]) continue;
 #pragma unroll
             for (int dt = 0; dt < 8; dt++)
 #pragma unroll
                 for (int vq = 0; vq < 4; vq++) {
                     const int d = 32 * dt + 8 * vq + 4 * kk;
-                    const float4 gv = *reinterpret_cast<const float4 *>(p.gate + base + d);
+                    const float4 g4 = gv[4 * dt + vq];
                     float4 out;
-                    out.x = o[rb][dt][4 * vq + 0] * inv * sigmoidf(gv.x);
-                    out.y = o[rb][dt][4 * vq + 1] * inv * sigmoidf(gv.y);
-                    out.z = o[rb][dt][4 * vq + 2] * inv * sigmoidf(gv.z);
-                    out.w = o[rb][dt][4 * vq + 3] * inv * sigmoidf(gv.w);
+                    out.x = o[rb][dt][4 * vq + 0] * inv * sigmoidf(g4.x);
+                    out.y = o[rb][dt][4 * vq + 1] * inv * sigmoidf(g4.y);
+                    out.z = o[rb][dt][4 * vq + 2] * inv * sigmoidf(g4.z);
+                    out.w = o[rb][dt][4 * vq + 3] * inv * sigmoidf(g4.w);
                     *reinterpret_cast<float4 *>(p.y + base + d) = out;
                 }
         }
