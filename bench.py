@@ -415,6 +415,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-reference-shapes", action="store_true",
+                    help="skip the timings at the reference's kernel shapes (profiling runs: the attention "
+                         "kernel's launches are then config 3's chunks only)")
     ap.add_argument("--decode-steps", type=int, default=256,
                     help="decode tokens per timed run (each over every layer); the counter runs "
                          "of the profiles use fewer: traffic per launch does not depend on it")
@@ -499,8 +502,9 @@ def main():
                      "counters": measured_counters(attn_kernel),
                      "flops_per_layer": flops},
     }
-    log("reference shapes: (0,33), (8192,2048), (27900,2048)")
-    result["reference_shapes"] = reference_shapes(work)
+    if not args.no_reference_shapes:
+        log("reference shapes: (0,33), (8192,2048), (27900,2048)")
+        result["reference_shapes"] = reference_shapes(work)
     device.reset_wall_timing(kernels_exact=True)
     for _ in range(args.steps):
         control.step()
