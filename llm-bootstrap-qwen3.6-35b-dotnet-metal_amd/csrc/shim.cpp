@@ -94,6 +94,7 @@ struct Context {
     hipError_t scratch_status = hipSuccess;
     uint64_t scratch_request = 0;   // bytes the last refused request asked for
     bool scratch_busy = false;      // the last request found the scratch held by another context
+    std::string workspace_error;    // the HIP error of the last failed workspace growth
     // serialized per-dispatch profiling (bridge.mm:61,198-204)
     bool profile = false;
     std::map<std::string, std::pair<double, uint64_t>> timings;
@@ -206,18 +207,28 @@ void *context_workspace(Context &c, uint64_t bytes) {
         return c.scratch;
     }
     if (bytes <= c.workspace_bytes) return c.workspace;
+    // A failed call's error is read back here, so that the launch check of a later dispatch
+    // (hipGetLastError) does not report it again, and kept for this dispatch's message.
+    auto failed = [&c](hipError_t e, const char *what) -> void * {
+        (void)hipGetLastError();
+        c.workspace_error = std::string(what) + ": " + hipGetErrorString(e);
+        return nullptr;
+    };
     // Grow: the old scratch may still be read by enqueued work.
-    if (hipStreamSynchronize(c.stream) != hipSuccess) return nullptr;
+    hipError_t e = hipStreamSynchronize(c.stream);
+    if (e != hipSuccess) return failed(e, "stream synchronize before the workspace grows");
     if (c.workspace) {
-        if (hipFree(c.workspace) != hipSuccess) return nullptr;
+        e = hipFree(c.workspace);
+        if (e != hipSuccess) return failed(e, "hipFree of the old workspace");
         c.allocated -= c.workspace_bytes;
     }
     c.workspace = nullptr;
     c.workspace_bytes = 0;
     uint64_t want = bytes < (64ull << 20) ? (64ull << 20) : bytes;
-    if (hipMalloc(&c.workspace, want) != hipSuccess) {
+    e = hipMalloc(&c.workspace, want);
+    if (e != hipSuccess) {
         c.workspace = nullptr;
-        return nullptr;
+        return failed(e, ("hipMalloc of " + std::to_string(want) + " bytes").c_str());
     }
     c.workspace_bytes = want;
     c.allocated += want;
@@ -509,6 +520,11 @@ int dispatch(Context *c, const char *name, void **buffers, const uint64_t *offse
         return fail(c, std::string(name) + ": split partials need " + std::to_string(asked) +
                            " bytes, more than the " + std::to_string(kStaticScratchBytes) +
                            "-byte static scratch of boot_dispatch_noalloc");
+    }
+    if (message && !c->workspace_error.empty()) {
+        const std::string detail = c->workspace_error;
+        c->workspace_error.clear();
+        return fail(c, std::string(name) + ": " + message + " (" + detail + ")");
     }
     if (message) return fail(c, std::string(name) + ": " + message);
     hipError_t e = hipGetLastError();
