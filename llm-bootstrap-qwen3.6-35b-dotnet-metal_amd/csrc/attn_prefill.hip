@@ -50,12 +50,12 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kTileRows = 256;             // logical rows per work-group (32 tokens x 8 heads)
 // Split partial of one work-group: O^T / l per row in region A ([256 rows][512 B]: the row in FP16,
 // or dimensions 0-127 in FP32) and region B (dimensions 128-255 of FP32 rows; the epilogue chooses
-// the format per wave), then m, l and vs_ref / 2^7 per row as floats, the last negated for FP32
+// the format per row), then m, l and vs_ref / 2^7 per row as floats, the last negated for FP32
 // rows. FP16 rows, the common case, are as compact as a plain FP16 partial.
 constexpr size_t kPartialRegion = (size_t)kTileRows * 512;
 constexpr size_t kPartialBytes = 2 * kPartialRegion + 3 * kTileRows * 4;
-// A wave's partials are FP16 when its outputs are at most this large (FP16's relative 2^-12 of 4
-// is 9.8e-4), FP32 otherwise.
+// A row's partial is FP16 when its outputs are at most this large (FP16's relative 2^-12 of 4 is
+// 9.8e-4), FP32 otherwise.
 constexpr float kNarrowPartial = 4.0f;
 
 struct PrefillParams {
@@ -945,8 +945,8 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
         return;
     }
     // Split partials: O^T / l per row, through LDS so that every store instruction writes 1 KB
-    // of whole rows (16-byte pieces of 32 rows each reach HBM as partial lines). A wave writes its
-    // 64 rows as FP16 when its largest |O^T / l| x vs_ref / 2^7 (an output magnitude) is at most
+    // of whole rows (16-byte pieces of 32 rows each reach HBM as partial lines). A row is written
+    // as FP16 when its largest |O^T / l| x vs_ref / 2^7 (an output magnitude) is at most
     // kNarrowPartial, where FP16's relative 2^-12 keeps the error under 1e-3; otherwise as FP32
     // (heavy-tailed V reaches |y| ~ 16: FP16 there is 4e-3 off, and no 16-bit format meets both
     // the 2e-3 bar and the reference's per-element bound for every value of such a row). Each row
@@ -962,10 +962,12 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
                                         : reinterpret_cast<unsigned char *>(qlds);
     unsigned char *pbase = reinterpret_cast<unsigned char *>(p.partial) +
                            (((size_t)g * p.tiles + tile) * p.splits + split) * kPartialBytes;
-    // FP16 rows are staged first, the wave's largest magnitude taken on the way; a wave whose
-    // outputs are too large then stages its rows again as FP32 from the accumulators
+    // Every row is staged as FP16 first, each row's largest magnitude taken on the way; the rows
+    // whose outputs are too large are then staged again as FP32 from the accumulators (chosen per
+    // row: with one choice per wave, a single element above the bound among a wave's 16K sent all
+    // 64 rows to FP32, 5 MB per 512-row chunk on the bench's data)
     typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-    float inv_l[2], zmax = 0.0f;
+    float inv_l[2], zmax[2] = {0.0f, 0.0f};
 #pragma unroll
     for (int rb = 0; rb < 2; rb++) {
         const int row = 32 * rb + i;   // of the wave's 64
@@ -977,14 +979,19 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
                 const int chunk = 4 * dt + vq;   // dimensions 8 chunk .. 8 chunk + 7; this lane's half at 4 kk
                 const float z0 = o[rb][dt][4 * vq] * inv_l[rb], z1 = o[rb][dt][4 * vq + 1] * inv_l[rb];
                 const float z2 = o[rb][dt][4 * vq + 2] * inv_l[rb], z3 = o[rb][dt][4 * vq + 3] * inv_l[rb];
-                zmax = max3f(zmax, max3f(fabsf(z0), fabsf(z1), fabsf(z2)), fabsf(z3));
+                zmax[rb] = max3f(zmax[rb], max3f(fabsf(z0), fabsf(z1), fabsf(z2)), fabsf(z3));
                 const half4 hv = {(_Float16)z0, (_Float16)z1, (_Float16)z2, (_Float16)z3};
                 *reinterpret_cast<half4 *>(ostage + row * 512 + ((chunk ^ (row & 31)) * 16) + 8 * kk) = hv;
             }
     }
+    // wide[rb]: bit i set when row 32 rb + i of the wave needs FP32 (lanes i and i + 32 hold its two
+    // halves of the dimensions)
+    uint32_t wide[2];
 #pragma unroll
-    for (int o2 = 32; o2 > 0; o2 >>= 1) zmax = fmaxf(zmax, __shfl_xor(zmax, o2, 64));
-    const bool wide = __builtin_amdgcn_readfirstlane(zmax * vs_out > kNarrowPartial ? 1u : 0u) != 0u;
+    for (int rb = 0; rb < 2; rb++) {
+        const float z = fmaxf(zmax[rb], __shfl_xor(zmax[rb], 32, 64));
+        wide[rb] = (uint32_t)__ballot(z * vs_out > kNarrowPartial);
+    }
     if (kk == 0) {
 #pragma unroll
         for (int rb = 0; rb < 2; rb++) {
@@ -992,11 +999,11 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
             float *stat = reinterpret_cast<float *>(pbase + 2 * kPartialRegion);
             stat[local_row] = m[rb];
             stat[kTileRows + local_row] = l[rb];
-            stat[2 * kTileRows + local_row] = wide ? -vs_out : vs_out;   // the sign carries the format
+            stat[2 * kTileRows + local_row] = (wide[rb] >> i) & 1u ? -vs_out : vs_out;   // the sign carries the format
         }
     }
     unsigned char *pw = pbase + (size_t)(64 * wave) * 512;   // the wave's rows are contiguous
-    if (!wide) {
+    if ((wide[0] | wide[1]) == 0u) {
 #pragma unroll
         for (int it = 0; it < 32; it++) {
             const int row = 2 * it + (lane >> 5), chunk = lane & 31;
@@ -1004,6 +1011,15 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
             *reinterpret_cast<uint4 *>(pw + (size_t)it * 1024 + lane * 16) = v;
         }
         return;
+    }
+    // some rows FP32: the FP16 rows first (iteration it stores rows 2 it and 2 it + 1, a half-wave
+    // each), then the FP32 rows of each row block that has any
+#pragma unroll
+    for (int it = 0; it < 32; it++) {
+        const int row = 2 * it + (lane >> 5), chunk = lane & 31;
+        if ((wide[it >> 4] >> (row & 31)) & 1u) continue;
+        const uint4 v = *reinterpret_cast<const uint4 *>(ostage + row * 512 + ((chunk ^ (row & 31)) * 16));
+        *reinterpret_cast<uint4 *>(pw + (size_t)it * 1024 + lane * 16) = v;
     }
     // (the accumulators are read by explicit moves, so that the compiler holds no vector-register
     // copies of them from the FP16 staging across the branch)
@@ -1014,6 +1030,7 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
     };
 #pragma unroll
     for (int rb = 0; rb < 2; rb++) {
+        if (wide[rb] == 0u) continue;   // wave-uniform
 #pragma unroll
         for (int dt = 0; dt < 8; dt++)
 #pragma unroll
@@ -1026,6 +1043,7 @@ __global__ __launch_bounds__(256, 1) void prefill_w64_kernel(PrefillParams p) {
             }
 #pragma unroll
         for (int r = 0; r < 32; r++) {   // lanes 0-31: dimensions 0-127 to region A, lanes 32-63 to B
+            if (((wide[rb] >> r) & 1u) == 0u) continue;   // wave-uniform
             const uint4 v = *reinterpret_cast<const uint4 *>(ostage + r * 1024 + ((lane ^ r) * 16));
             *reinterpret_cast<uint4 *>(pw + (lane >> 5) * kPartialRegion + (size_t)(32 * rb + r) * 512 + (lane & 31) * 16) = v;
         }
