@@ -49,8 +49,11 @@ def run_prefill(device, q, gate, cache, rows, history, alias=False, kernel="atte
 # 262144-token window (ContextLimits.cs:5); (0, 33), (8192, 2048), (27900, 2048): the shapes the
 # reference times its INT8 online kernel at (docs/INT8_30K_PREFILL_20261104.md:59-61), 2048 rows
 # being the chunk its tuned preset dispatches (Program.cs:71, Prefill.cs:111-121)
+# (9000, 500) and (5000, 100): split chunks whose last 256-row tile is partial, with a row tile's
+# splits on one XCD (the combine's blocks skip the rows past the chunk); (4093, 7) and (262080, 64)
+# take the other two block placements
 PREFILL_CASES = [(0, 1), (17, 7), (127, 31), (127, 32), (257, 33), (4093, 7), (8192, 128), (0, 512), (3584, 512),
-                 (30000, 33), (30208, 512), (262080, 64), (0, 33), (8192, 2048), (27900, 2048)]
+                 (30000, 33), (30208, 512), (262080, 64), (0, 33), (8192, 2048), (27900, 2048), (9000, 500), (5000, 100)]
 
 
 @pytest.mark.parametrize("history,rows", PREFILL_CASES)
