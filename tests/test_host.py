@@ -3,6 +3,7 @@ host KV policy mirrors the engine's constants and rules (Program.cs:307-320)."""
 import ctypes
 import os
 import re
+import sys
 
 import pytest
 
@@ -138,3 +139,14 @@ def test_rope_frequencies_are_correctly_rounded():
             nearest = min((np.nextafter(f, np.float32(-1)), f, np.nextafter(f, np.float32(2))),
                           key=lambda c: abs(Decimal(float(c)) - exact))
             assert host == nearest, (theta, j)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py --gpus N with N > 1 exits with status 2 and says why, before touching a device."""
+    import json
+    import subprocess
+    out = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                         text=True, timeout=120)
+    assert out.returncode == 2
+    line = json.loads(out.stdout.strip().splitlines()[-1])
+    assert line["n_gpus"] == 2 and "one GPU" in line["error"]
