@@ -56,6 +56,28 @@ PREFILL_CASES = [(0, 1), (17, 7), (127, 31), (127, 32), (257, 33), (4093, 7), (8
                  (30000, 33), (30208, 512), (262080, 64), (0, 33), (8192, 2048), (27900, 2048), (9000, 500), (5000, 100)]
 
 
+# A seeded sweep of chunk shapes: rows across 256-row tile edges (1 to 511 rows: one to eight
+# row tiles, full and partial) at histories up to 12000, so that split counts from 1 to 64 and
+# each of the three block placements (a row tile's splits on one XCD, a key range's blocks on one
+# XCD, plain order) meet partial tiles and ragged last splits.
+SWEEP_ROWS = [1, 7, 31, 32, 33, 64, 97, 128, 129, 200, 255, 256, 300, 384, 511]
+SWEEP_CASES = [(int(h), r) for h, r in zip(np.random.default_rng(2026).integers(0, 12000, len(SWEEP_ROWS)), SWEEP_ROWS)]
+
+
+@pytest.mark.parametrize("history,rows", SWEEP_CASES)
+def test_prefill_shape_sweep(device, oracle, history, rows):
+    q, gate, host = build_case(oracle, history, rows)
+    cache = upload_cache(device, *host)
+    y = run_prefill(device, q, gate, cache, rows, history)
+    assert np.isnan(y[-1]), "output guard overwritten"
+    y = y[:-1]
+    ref, bound = oracle.attention(q, *host, gate, rows, history, round_q_half=1, with_bound=True)
+    err = np.abs(y - ref)
+    assert rel_l2(y, ref) <= REL_L2 and err.max() <= MAX_ABS, (rel_l2(y, ref), err.max())
+    assert np.all(err <= bound / 256 + 1e-4)
+    cache.dispose()
+
+
 @pytest.mark.parametrize("history,rows", PREFILL_CASES)
 def test_prefill_matches_fp64(device, oracle, history, rows):
     q, gate, host = build_case(oracle, history, rows)
