@@ -268,6 +268,26 @@ def test_decode_matches_fp64(device, oracle, history, rows, path):
     cache.dispose()
 
 
+# A seeded sweep of the fused decode: 1 to 64 rows (each causal at its own position) at
+# histories up to 60000, so that split counts, chunk and page edges and the rows' ragged ends vary
+DECODE_SWEEP_ROWS = [1, 1, 2, 3, 5, 8, 13, 16, 31, 47, 64, 64]
+DECODE_SWEEP_CASES = [(int(h), r) for h, r in
+                      zip(np.random.default_rng(2027).integers(0, 60000, len(DECODE_SWEEP_ROWS)), DECODE_SWEEP_ROWS)]
+
+
+@pytest.mark.parametrize("history,rows", DECODE_SWEEP_CASES)
+def test_decode_shape_sweep(device, oracle, history, rows):
+    q, gate, host = build_case(oracle, history, rows)
+    cache = upload_cache(device, *host)
+    y = run_decode(device, q, gate, cache, rows, history, path="fused")
+    assert np.isnan(y[-1])
+    y = y[:-1]
+    ref = oracle.attention(q, *host, gate, rows, history, round_q_half=0)
+    err = np.abs(y - ref)
+    assert rel_l2(y, ref) <= REL_L2 and err.max() <= MAX_ABS, (rel_l2(y, ref), err.max())
+    cache.dispose()
+
+
 @pytest.mark.parametrize("history,rows,spikes", [
     # a 131072-token context: 1152-token splits of nine 128-token chunks, spikes in later
     # chunks of the first split, mid-context and at the end

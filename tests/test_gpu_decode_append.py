@@ -23,7 +23,12 @@ def layer_from(device, host):
 # 131072-token one every 1152 (9 chunks); 262143 is the window's last position. 130181 and
 # 130309 fall in 8-chunk splits at token 5 of the split's chunk 1 and chunk 2, whose registers
 # are loaded before the key loop and patched there
-@pytest.mark.parametrize("pos", [0, 1, 127, 128, 255, 256, 1151, 1152, 4093, 130181, 130309, 131071, 131072, 262143])
+# plus a seeded draw of eight positions up to 200000 (the new token anywhere in its split)
+SWEEP = [int(x) for x in np.random.default_rng(2028).integers(1, 200000, 8)]
+
+
+@pytest.mark.parametrize("pos", [0, 1, 127, 128, 255, 256, 1151, 1152, 4093, 130181, 130309, 131071, 131072, 262143]
+                         + SWEEP)
 def test_decode_append_equals_two_dispatches(device, oracle, pos):
     capacity = pos + 1
     k, v = outlier_kv(oracle, pos, seed=80) if pos else (np.zeros((0, 2, 256), np.float32),) * 2
