@@ -59,6 +59,20 @@ def test_append_positions_and_guards(device, oracle, pos, rows):
     assert_same_bytes(*run_store(device, oracle, k, v, pos))
 
 
+# A seeded sweep of (position, rows): starts anywhere in a page, 1 to 9000 rows (both tile sizes,
+# partial tiles at either end), Student-t K/V
+APPEND_SWEEP = [(int(p), int(r)) for p, r in zip(np.random.default_rng(2029).integers(0, 250000, 10),
+                                                 [1, 3, 16, 17, 255, 257, 1023, 4095, 4097, 9000])]
+
+
+@pytest.mark.parametrize("pos,rows", APPEND_SWEEP)
+def test_append_shape_sweep(device, oracle, pos, rows):
+    rng = np.random.default_rng(pos + rows)
+    k = rng.standard_t(4, (rows, 2, 256)).astype(np.float32)
+    v = rng.standard_t(4, (rows, 2, 256)).astype(np.float32)
+    assert_same_bytes(*run_store(device, oracle, k, v, pos))
+
+
 def test_append_special_values(device, oracle):
     rows = 8
     k = np.zeros((rows, 2, 256), np.float32)
