@@ -173,11 +173,15 @@ def reference_shapes(work: PrefillWorkload, runs: int = 20):
             ws.encode_int8(None, layer.key, layer.value, layer.key_scale, layer.value_scale, gate, out, rows, history,
                            prepared_query=True)
         d.end()
-        ks = kernel_stats(d, ["prefill_w64_kernel", "prefill_combine_kernel"])
-        attn = ks["prefill_w64_kernel"][0] / runs
-        comb = ks.get("prefill_combine_kernel", (0.0, 0))[0] / runs
+        # chunks of at most 64 rows over a short history run on the decode kernel (its grouped FP16
+        # query variant) and, when split, its combine
+        ks = kernel_stats(d, ["prefill_w64_kernel", "prefill_combine_kernel", "decode_int8_half_query_kernel",
+                              "decode_combine_kernel"])
+        kernel = "prefill_w64_kernel" if "prefill_w64_kernel" in ks else "decode_int8_half_query_kernel"
+        attn = ks[kernel][0] / runs
+        comb = sum(ks.get(n, (0.0, 0))[0] for n in ("prefill_combine_kernel", "decode_combine_kernel")) / runs
         flops = prefill_flops(history, rows)
-        entries.append({"history": history, "rows": rows, "attention_kernel_ms": round(attn, 5),
+        entries.append({"history": history, "rows": rows, "kernel": kernel, "attention_kernel_ms": round(attn, 5),
                         "combine_ms": round(comb, 5), "ms": round(attn + comb, 5),
                         "mfma_frac_attention_kernel": round(flops / (attn * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
                         "reference_m5pro_gpu_median_ms": m5})
@@ -185,7 +189,8 @@ def reference_shapes(work: PrefillWorkload, runs: int = 20):
         b.dispose()
     ws.dispose()
     return {"what": "attention_online_int8_q32_k256_r2 at the reference's timed shapes (history, query rows), "
-                    f"kernel-exact, mean of {runs} launches over config 3's cache; the reference's figures are GPU "
+                    f"kernel-exact (the kernel that served the shape and its split combine), mean of {runs} launches "
+                    f"over config 3's cache; the reference's figures are GPU "
                     "medians on an Apple M5 Pro (docs/INT8_30K_PREFILL_20261104.md:59-61), context only",
             "shapes": entries}
 

@@ -131,7 +131,7 @@ constexpr int kMaxDecodeSplits = 1024;
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct DecodeParams {
-    const float *q;
+    const float *q;              // FP32 [rows][16][256] (or qh below)
     const int8_t *k;
     const int8_t *v;
     const float *ks;
@@ -150,6 +150,7 @@ struct DecodeParams {
     float *rotated;              // FP32 [16][256]
     int8_t *k_out, *v_out;
     float *ks_out, *vs_out;
+    const _Float16 *qh;          // prefill chunks routed here: the grouped FP16 query [2][rows][8][256]
 };
 
 // sigmoid(x) = 1 / (1 + 2^(-x log2(e))) with the hardware exponential and reciprocal (about an ulp
@@ -328,6 +329,7 @@ __device__ __attribute__((always_inline)) inline void patch_v(VRegs &r, int tid,
 // vs_ref split into FP16 hi + lo; vs_ref, the split's largest V scale, keeps Px below
 // 256 and multiplies the result once. Lane l holds MFMA column n = l % 16 and
 // token/k group qq = l / 16.
+template <bool kHalfQ>
 __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
     typedef int v4i __attribute__((ext_vector_type(4)));
     typedef _Float16 half4 __attribute__((ext_vector_type(4)));
@@ -381,16 +383,28 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
     // n % 8 (waves 4-7 load the same chunks and only waves 0-3 publish them)
     const int chunk = wave & 3;
     float4 x[4];
-    {
-        const float *qh = p.q + ((size_t)row * 16 + g * 8 + head) * 256 + 64 * chunk + 16 * qq;
+    if constexpr (kHalfQ) {
+        // the prefill path's grouped FP16 query, [(g rows + row) 8 + head][256]: exact in FP32
+        const _Float16 *qs = p.qh + (((size_t)g * p.rows + row) * 8 + head) * 256 + 64 * chunk + 16 * qq;
+        const half8 a = *reinterpret_cast<const half8 *>(qs), b = *reinterpret_cast<const half8 *>(qs + 8);
+        x[0] = make_float4((float)a[0], (float)a[1], (float)a[2], (float)a[3]);
+        x[1] = make_float4((float)a[4], (float)a[5], (float)a[6], (float)a[7]);
+        x[2] = make_float4((float)b[0], (float)b[1], (float)b[2], (float)b[3]);
+        x[3] = make_float4((float)b[4], (float)b[5], (float)b[6], (float)b[7]);
+    } else {
+        const float *qs = p.q + ((size_t)row * 16 + g * 8 + head) * 256 + 64 * chunk + 16 * qq;
 #pragma unroll
-        for (int f = 0; f < 4; f++) x[f] = *reinterpret_cast<const float4 *>(qh + 4 * f);
+        for (int f = 0; f < 4; f++) x[f] = *reinterpret_cast<const float4 *>(qs + 4 * f);
     }
     // append mode: head `wave` of the group in rope4's layout (dims 4 lane .. +3) and the new
     // token's K and V of the group. Loaded in every mode and every wave (from the query itself
     // when there is no new token): a fixed count of loads keeps the counter waits exact.
-    const float *knew = p.append ? p.knew : p.q, *vnew = p.append ? p.vnew : p.q;
-    const float4 rq = *reinterpret_cast<const float4 *>(p.q + ((size_t)row * 16 + g * 8 + wave) * 256 + 4 * lane);
+    // (the FP16 query path has no FP32 query and no new token: its first 2 KB, in range for any
+    // row count, stand in for these unused loads)
+    const float *qf = kHalfQ ? reinterpret_cast<const float *>(p.qh) : p.q;
+    const float *knew = p.append ? p.knew : qf, *vnew = p.append ? p.vnew : qf;
+    const float4 rq = *reinterpret_cast<const float4 *>(
+        kHalfQ ? qf + 4 * lane : p.q + ((size_t)row * 16 + g * 8 + wave) * 256 + 4 * lane);
     const float4 nk = *reinterpret_cast<const float4 *>(knew + (size_t)g * 256 + 4 * lane);
     const float4 nv = *reinterpret_cast<const float4 *>(vnew + (size_t)g * 256 + 4 * lane);
     // every wave's small loads enter the CU's memory pipeline before any chunk load
@@ -885,6 +899,7 @@ namespace {
 // Split geometry shared by both decode entry points: whole 128-token chunks per split, chosen so
 // that the grid (splits x 2 groups x rows, one work-group per CU) fits the CUs in one round (a
 // second, nearly empty round would double the time), at most kMaxSplitTokens per split.
+template <bool kHalfQ = false>
 const char *decode_launch(Context &c, DecodeParams &d, uint64_t rows, uint64_t length) {
     const uint64_t total_chunks = (length + kChunk - 1) / kChunk;
     const uint64_t slots = std::max<uint64_t>(1, (uint64_t)std::max(1, context_cus(c)) / (2 * rows));
@@ -900,7 +915,8 @@ const char *decode_launch(Context &c, DecodeParams &d, uint64_t rows, uint64_t l
         d.partial = (float *)context_workspace(c, rows * 2 * splits * kPartialFloats * sizeof(float));
         BOOT_REQUIRE(d.partial, "cannot allocate decode split workspace");
     }
-    launch_timed(c, "decode_int8_kernel", decode_int8_kernel, dim3((uint32_t)splits, 2, (uint32_t)rows), dim3(512), d);
+    launch_timed(c, kHalfQ ? "decode_int8_half_query_kernel" : "decode_int8_kernel", decode_int8_kernel<kHalfQ>,
+                 dim3((uint32_t)splits, 2, (uint32_t)rows), dim3(512), d);
     if (splits > 1) {
         context_split(c, "attention_decode_int8.combine");
         launch_timed(c, "decode_combine_kernel", decode_combine_kernel, dim3(4, 16, (uint32_t)rows), dim3(256), d.partial,
@@ -933,6 +949,7 @@ const char *launch_decode_append_int8(Context &c, const View *b, int count, cons
                  "bindings misaligned (q, k, v, rotated, kc, vc need 16 bytes)");
     DecodeParams d;
     d.q = (const float *)b[0].ptr;
+    d.qh = nullptr;
     d.knew = (const float *)b[1].ptr;
     d.vnew = (const float *)b[2].ptr;
     d.rotated = (float *)b[3].ptr;
@@ -971,6 +988,7 @@ const char *launch_decode_int8(Context &c, const View *b, int count, const boot_
                  "bindings misaligned (q, k, v need 16 bytes)");
     DecodeParams d;
     d.q = (const float *)b[0].ptr;
+    d.qh = nullptr;
     d.k = (const int8_t *)b[1].ptr;
     d.v = (const int8_t *)b[2].ptr;
     d.gate = (const float *)b[3].ptr;
@@ -985,6 +1003,32 @@ const char *launch_decode_int8(Context &c, const View *b, int count, const boot_
     d.k_out = d.v_out = nullptr;
     d.ks_out = d.vs_out = nullptr;
     return decode_launch(c, d, rows, length);
+}
+
+const char *launch_online_int8_as_decode(Context &c, const View *b, const boot_kernel_args &p) {
+    // A prefill chunk of at most 64 rows over a short history (launch_prefill's choice, which has
+    // validated the bindings: grouped FP16 q, k, v, gate, y, ks, vs): one work-group per (row, KV
+    // group, split) streams the keys up to its own row's position, as a decode of that many rows,
+    // instead of 256-row tiles that are mostly empty.
+    const uint64_t rows = p.m, length = (uint64_t)p.pos + rows;
+    BOOT_REQUIRE(rows >= 1 && rows <= 64, "a prefill chunk served by the decode kernel has 1 to 64 rows");
+    DecodeParams d;
+    d.q = nullptr;
+    d.qh = (const _Float16 *)b[0].ptr;
+    d.k = (const int8_t *)b[1].ptr;
+    d.v = (const int8_t *)b[2].ptr;
+    d.gate = (const float *)b[3].ptr;
+    d.y = (float *)b[4].ptr;
+    d.ks = (const float *)b[5].ptr;
+    d.vs = (const float *)b[6].ptr;
+    d.pos = p.pos;
+    d.append = 0;
+    d.freq = RopeFreq{};
+    d.knew = d.vnew = nullptr;
+    d.rotated = nullptr;
+    d.k_out = d.v_out = nullptr;
+    d.ks_out = d.vs_out = nullptr;
+    return decode_launch<true>(c, d, rows, length);
 }
 
 }  // namespace boot

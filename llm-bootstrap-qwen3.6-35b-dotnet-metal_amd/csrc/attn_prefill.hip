@@ -57,6 +57,8 @@ constexpr size_t kPartialBytes = 2 * kPartialRegion + 3 * kTileRows * 4;
 // A row's partial is FP16 when its outputs are at most this large (FP16's relative 2^-12 of 4 is
 // 9.8e-4), FP32 otherwise.
 constexpr float kNarrowPartial = 4.0f;
+// Prefill chunks of at most 64 rows with rows x keys up to this go through the decode kernel.
+constexpr uint64_t kDecodeRouteWork = 65536;
 
 struct PrefillParams {
     const _Float16 *q;      // grouped FP16 [2][M][8][256]
@@ -1163,6 +1165,11 @@ const char *launch_prefill(Context &c, const View *b, const boot_kernel_args &a,
     BOOT_REQUIRE(aligned(b[0].ptr, 16) && aligned(b[1].ptr, 16) && aligned(b[2].ptr, 16) && aligned(b[3].ptr, 16) &&
                      aligned(b[4].ptr, 16),
                  "bindings misaligned (q, k, v, gate, y need 16 bytes)");
+    // Chunks of at most 64 rows whose rows x keys stay within kDecodeRouteWork go to the decode
+    // kernel (one work-group per row, KV group and split of the keys): at (0, 33) 7.6 against
+    // 25.4 us, at (2048, 33) 24.8 against 38.4 us; each row reads the keys again, so at (8192, 33)
+    // it would take 81 against 44 us.
+    if (int8 && rows <= 64 && rows * keys <= kDecodeRouteWork) return launch_online_int8_as_decode(c, b, a);
     PrefillParams p;
     p.q = (const _Float16 *)b[0].ptr;
     p.k = b[1].ptr;

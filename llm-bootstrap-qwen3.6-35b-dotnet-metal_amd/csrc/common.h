@@ -87,6 +87,9 @@ const char *launch_online_fp16(Context &, const View *, int, const boot_kernel_a
 const char *launch_batch_rope_half(Context &, const View *, int, const boot_kernel_args &, const uint32_t *);
 const char *launch_prepare_fused_half(Context &, const View *, int, const boot_kernel_args &, const uint32_t *);
 const char *launch_decode_int8(Context &, const View *, int, const boot_kernel_args &, const uint32_t *);
+// attention_online_int8 for chunks of at most 64 rows over a short history, through the decode
+// kernel (bindings validated by the prefill launcher)
+const char *launch_online_int8_as_decode(Context &, const View *, const boot_kernel_args &);
 const char *launch_decode_append_int8(Context &, const View *, int, const boot_kernel_args &, const uint32_t *);
 const char *launch_scores_int8(Context &, const View *, int, const boot_kernel_args &, const uint32_t *);
 const char *launch_softmax(Context &, const View *, int, const boot_kernel_args &, const uint32_t *);

@@ -60,7 +60,7 @@ def prefill(device, q, gate, cache, rows, history, noalloc):
 
 @pytest.mark.parametrize("kind,cases", [
     ("decode", [(131071, 1), (4093, 7)]),        # 114 splits per group, then 6
-    ("prefill", [(30208, 512), (257, 33)]),      # 68 MB of partial slots, then 8 splits of one tile
+    ("prefill", [(30208, 512), (257, 33)]),      # 68 MB of partial slots, then a 33-row chunk (decode kernel, 3 splits)
 ])
 def test_noalloc_matches_dispatch(oracle, kind, cases):
     """A fresh context: every no-allocation call runs before the context has a workspace, so a
