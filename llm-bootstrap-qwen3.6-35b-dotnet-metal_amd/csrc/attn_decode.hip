@@ -79,45 +79,218 @@ __device__ inline float block_reduce_256(float v, float *partial, bool is_max) {
     return r;
 }
 
-// In-place three-pass softmax over i <= pos of each row (kernels.metal:163-166).
-__global__ __launch_bounds__(256) void softmax_kernel(float *__restrict__ x, uint32_t K, uint32_t pos) {
+// In-place softmax over i <= pos of each row of stride K (kernels.metal:163-166), in two passes
+// over chunks of kSoftmaxChunk elements (absolute boundaries, so that a row's result does not
+// depend on how many rows the dispatch holds): the chunk's maximum and its sum of exp(x - max),
+// then, per chunk, the row's maximum M and sum L merged from those in chunk order and
+// x = exp(x - M) / L. Elements past pos are left as they are.
+constexpr int kSoftmaxChunk = 8192;
+constexpr int kSoftmaxPer = kSoftmaxChunk / 256;
+
+__global__ __launch_bounds__(256) void softmax_stats_kernel(const float *__restrict__ x, float2 *__restrict__ stats,
+                                                            uint32_t K, uint32_t pos, uint32_t chunks) {
     __shared__ float partial[4];
-    float *r = x + (size_t)blockIdx.x * K;
+    const uint32_t c = blockIdx.x, r = blockIdx.y;
+    const float *row = x + (size_t)r * K;
+    const uint32_t lo = c * kSoftmaxChunk, hi = min(pos + 1, lo + kSoftmaxChunk);
+    float e[kSoftmaxPer];
+#pragma unroll
+    for (int j = 0; j < kSoftmaxPer; j++) {
+        const uint32_t i = lo + threadIdx.x + 256 * j;
+        e[j] = i < hi ? row[i] : -INFINITY;
+    }
     float top = -INFINITY;
-    for (uint32_t i = threadIdx.x; i <= pos; i += 256) top = fmaxf(top, r[i]);
+#pragma unroll
+    for (int j = 0; j < kSoftmaxPer; j++) top = fmaxf(top, e[j]);
     top = block_reduce_256(top, partial, true);
     float sum = 0.0f;
-    for (uint32_t i = threadIdx.x; i <= pos; i += 256) {
-        const float value = expf(r[i] - top);
-        r[i] = value;
-        sum += value;
-    }
+    if (top != -INFINITY)
+#pragma unroll
+        for (int j = 0; j < kSoftmaxPer; j++) sum += expf(e[j] - top);
     sum = block_reduce_256(sum, partial, false);
-    for (uint32_t i = threadIdx.x; i <= pos; i += 256) r[i] /= sum;
+    if (threadIdx.x == 0) stats[(size_t)r * chunks + c] = make_float2(top, sum);
 }
 
-// y[(row*16+h)*256+d] = sum_t scores*vs*vcode * sigmoid(gate) (kernels.metal:153-156).
-__global__ __launch_bounds__(256) void values_int8_kernel(const float *__restrict__ scores, const int8_t *__restrict__ v,
-                                                          const float *__restrict__ gate, float *__restrict__ y,
-                                                          const float *__restrict__ vs, uint32_t rows, uint32_t K,
-                                                          uint32_t pos) {
-    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= rows * 4096) return;
-    const uint32_t row = i / 4096, h = (i % 4096) / 256, d = i % 256, g = h / 8;
-    const float *s = scores + ((size_t)row * 16 + h) * K;
-    const uint32_t end = pos + row + 1;
+__global__ __launch_bounds__(256) void softmax_apply_kernel(float *__restrict__ x, const float2 *__restrict__ stats,
+                                                            uint32_t K, uint32_t pos, uint32_t chunks) {
+    const uint32_t c = blockIdx.x, r = blockIdx.y;
+    const float2 *st = stats + (size_t)r * chunks;
+    float top = -INFINITY;
+    for (uint32_t k = 0; k < chunks; k++) top = fmaxf(top, st[k].x);
     float sum = 0.0f;
-    uint32_t t = 0;
-    for (; t + 16 <= end && ((t & 255) + 16 <= 256); t += 16) {
-        const uint4 w = *reinterpret_cast<const uint4 *>(v + value_index((uint64_t)t * 2 + g, d));
-        const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+    for (uint32_t k = 0; k < chunks; k++)
+        if (st[k].x != -INFINITY) sum += st[k].y * expf(st[k].x - top);
+    float *row = x + (size_t)r * K;
+    const uint32_t lo = c * kSoftmaxChunk, hi = min(pos + 1, lo + kSoftmaxChunk);
+    float e[kSoftmaxPer];
 #pragma unroll
-        for (int j = 0; j < 16; j++) {
-            const float code = (float)(int8_t)((words[j >> 2] >> (8 * (j & 3))) & 0xff);
-            sum += s[t + j] * vs[(size_t)(t + j) * 2 + g] * code;
+    for (int j = 0; j < kSoftmaxPer; j++) {
+        const uint32_t i = lo + threadIdx.x + 256 * j;
+        e[j] = i < hi ? row[i] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < kSoftmaxPer; j++) {
+        const uint32_t i = lo + threadIdx.x + 256 * j;
+        if (i < hi) row[i] = expf(e[j] - top) / sum;
+    }
+}
+
+// y[(row*16+h)*256+d] = sum_{t <= pos+row} scores*vs*vcode * sigmoid(gate) (kernels.metal:153-156),
+// split over absolute kValuesSplit-token ranges (a row's sum does not depend on the dispatch's
+// row count); values_combine_kernel adds the splits in order and applies the gate.
+constexpr int kValuesSplit = 512;
+
+// Work-group (split, KV group, kRows rows): O^T[d][c] += V^T[d][t] B[t][c] on
+// v_mfma_f32_16x16x16_f16 with the codes exact in FP16 and, per row, B = p * vs / vs_r in the
+// 16 columns 8 heads x {FP16 hi, FP16 lo} (vs_r the row's largest V scale over its tokens of the
+// split, so that B <= 1; hi + lo keeps about 22 bits), the result times vs_r. Wave w takes
+// dimensions 64w .. 64w + 63; a 64-token block is four k-steps, lane (n, qq) of step s holding
+// tokens 16qq + 4s .. + 3 of the block for both operands (one 16-byte code load per dimension
+// tile covers its four steps), and the next block's loads are issued before the current block is
+// staged. Every quantity of a row depends on that row's range only, whatever kRows is.
+constexpr int kVmBlock = 64;
+
+template <int kRows>
+__global__ __launch_bounds__(256) void values_partial_kernel(const float *__restrict__ scores,
+                                                             const int8_t *__restrict__ v, const float *__restrict__ vs,
+                                                             float *__restrict__ partial, uint32_t rows, uint32_t K,
+                                                             uint32_t pos, uint32_t splits) {
+    typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+    constexpr int kEnt = 2 * kRows;                    // staging (row, head) pairs per thread, one token each
+    __shared__ uint2 bs[kRows][4][64];                  // B operands [row][k-step][lane]
+    __shared__ float vred[4][kRows];
+    const uint32_t split = blockIdx.x, g = blockIdx.y, r0 = blockIdx.z * kRows;
+    const uint32_t nr = min((uint32_t)kRows, rows - r0);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n = lane & 15, qq = lane >> 4;
+    const uint32_t t0 = split * kValuesSplit;
+    const uint32_t t1 = min(pos + r0 + nr, t0 + kValuesSplit);   // the work-group's last row's end
+    // each row's largest V scale over its tokens of the split
+    float vr[kRows];
+    {
+        float vm[kRows];
+#pragma unroll
+        for (int r = 0; r < kRows; r++) vm[r] = 0.0f;
+        if (t0 < t1)
+#pragma unroll
+            for (int k = 0; k < kValuesSplit / 256; k++) {
+                const uint32_t t = t0 + tid + 256 * k;
+                const float x = vs[(size_t)min(t, t1 - 1) * 2 + g];
+#pragma unroll
+                for (int r = 0; r < kRows; r++)
+                    if (t < pos + r0 + r + 1) vm[r] = fmaxf(vm[r], x);
+            }
+#pragma unroll
+        for (int r = 0; r < kRows; r++) {
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) vm[r] = fmaxf(vm[r], __shfl_xor(vm[r], o, 64));
+            if (lane == 0) vred[wave][r] = vm[r];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < kRows; r++) vr[r] = fmaxf(fmaxf(vred[0][r], vred[1][r]), fmaxf(vred[2][r], vred[3][r]));
+    }
+    floatx4 acc[4][kRows];
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+        for (int r = 0; r < kRows; r++) acc[dt][r] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    // staging: thread T takes token T % 64 of the block for the (row, head) pairs T / 64 + 4i, so that
+    // a wave's score loads read 64 consecutive tokens of one pair
+    const int tok = tid & 63, pair0 = tid >> 6;
+    struct Loads {
+        float sc[kEnt], sv;
+        uint4 w4[4];   // the wave's four dimension tiles: dimension 64 wave + 16 dt + n, tokens 16 qq .. + 15
+    };
+    auto load = [&](Loads &L, uint32_t tb) __attribute__((always_inline)) {
+        const uint32_t t = tb + tok;
+        L.sv = vs[(size_t)min(t, t1 - 1) * 2 + g];
+#pragma unroll
+        for (int i = 0; i < kEnt; i++) {
+            const int rh = pair0 + 4 * i, r = rh >> 3, h = rh & 7;
+            const bool live = (uint32_t)r < nr && t < pos + r0 + r + 1;
+            L.sc[i] = live ? scores[((size_t)(r0 + r) * 16 + g * 8 + h) * K + t] : 0.0f;
+        }
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++)
+            L.w4[dt] = *reinterpret_cast<const uint4 *>(v + value_index((uint64_t)tb * 2 + g, 64 * wave + 16 * dt + n) + 16 * qq);
+    };
+    Loads cur, nxt;
+    if (t0 < t1) load(cur, t0);
+    for (uint32_t tb = t0; tb < t1; tb += kVmBlock) {
+        const bool more = tb + kVmBlock < t1;   // work-group-uniform
+        if (more) load(nxt, tb + kVmBlock);
+        __syncthreads();   // the previous block's B reads are done
+        {
+            // token tok of the block is k = 4 (tok / 16) + tok % 4 of step (tok % 16) / 4: half tok % 4
+            // of lane 16 (tok / 16) + column
+            const int s = (tok & 15) >> 2, j = tok & 3, lrow = 16 * (tok >> 4);
+#pragma unroll
+            for (int i = 0; i < kEnt; i++) {
+                const int rh = pair0 + 4 * i, r = rh >> 3, h = rh & 7;
+                if ((uint32_t)r < nr) {
+                    const float inv = vr[r] > 0.0f ? 1.0f / vr[r] : 0.0f;
+                    const float x = cur.sc[i] * cur.sv * inv;
+                    const _Float16 hi = (_Float16)x, lo = (_Float16)(x - (float)hi);
+                    reinterpret_cast<_Float16 *>(&bs[r][s][lrow + h])[j] = hi;
+                    reinterpret_cast<_Float16 *>(&bs[r][s][lrow + h + 8])[j] = lo;
+                }
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            half4 a[4];
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++) {
+                const uint4 &w = cur.w4[dt];
+                const uint32_t word = s == 0 ? w.x : s == 1 ? w.y : s == 2 ? w.z : w.w;
+                uint32_t h0, h1;
+                i8x4_to_f16(word, h0, h1);
+                a[dt] = __builtin_bit_cast(half4, make_uint2(h0, h1));
+            }
+#pragma unroll
+            for (int r = 0; r < kRows; r++) {
+                if ((uint32_t)r >= nr) break;   // uniform
+                const half4 b = __builtin_bit_cast(half4, bs[r][s][lane]);
+#pragma unroll
+                for (int dt = 0; dt < 4; dt++) acc[dt][r] = __builtin_amdgcn_mfma_f32_16x16x16f16(a[dt], b, acc[dt][r], 0, 0, 0);
+            }
+        }
+        if (more) cur = nxt;
+    }
+    // the lo column n + 8 joins the hi column n (head n); lanes n < 8 write dimensions 64 wave + 16 dt + 4 qq + e
+#pragma unroll
+    for (int r = 0; r < kRows; r++) {
+        if ((uint32_t)r >= nr) break;
+        float *out = partial + (((size_t)(r0 + r) * 2 + g) * splits + split) * 2048;
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) {
+            float4 o4;
+            o4.x = (acc[dt][r][0] + __shfl_xor(acc[dt][r][0], 8, 64)) * vr[r];
+            o4.y = (acc[dt][r][1] + __shfl_xor(acc[dt][r][1], 8, 64)) * vr[r];
+            o4.z = (acc[dt][r][2] + __shfl_xor(acc[dt][r][2], 8, 64)) * vr[r];
+            o4.w = (acc[dt][r][3] + __shfl_xor(acc[dt][r][3], 8, 64)) * vr[r];
+            if (n < 8) *reinterpret_cast<float4 *>(out + n * 256 + 64 * wave + 16 * dt + 4 * qq) = o4;
         }
     }
-    for (; t < end; t++) sum += s[t] * vs[(size_t)t * 2 + g] * (float)v[value_index((uint64_t)t * 2 + g, d)];
+}
+
+__global__ __launch_bounds__(256) void values_combine_kernel(const float *__restrict__ partial,
+                                                             const float *__restrict__ gate, float *__restrict__ y,
+                                                             uint32_t splits) {
+    const uint32_t h = blockIdx.x, row = blockIdx.y, g = h / 8, d = threadIdx.x;
+    const float *src = partial + ((size_t)row * 2 + g) * splits * 2048 + (h % 8) * 256 + d;
+    float sum = 0.0f;
+    uint32_t s = 0;
+    for (; s + 8 <= splits; s += 8) {   // eight loads in flight, added in split order
+        float x[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) x[u] = src[(size_t)(s + u) * 2048];
+#pragma unroll
+        for (int u = 0; u < 8; u++) sum += x[u];
+    }
+    for (; s < splits; s++) sum += src[(size_t)s * 2048];
+    const size_t i = ((size_t)row * 16 + h) * 256 + d;
     y[i] = sum * (1.0f / (1.0f + expf(-gate[i])));
 }
 
@@ -871,7 +1044,16 @@ const char *launch_softmax(Context &c, const View *b, int count, const boot_kern
     BOOT_REQUIRE(p.pos < K, "softmax position must be below the row stride K");
     BOOT_REQUIRE(b[0].bytes >= groups * K * 4, "scores buffer smaller than groups*K floats");
     BOOT_REQUIRE(aligned(b[0].ptr, 4), "scores binding misaligned");
-    softmax_kernel<<<(uint32_t)groups, 256, 0, context_stream(c)>>>((float *)b[0].ptr, (uint32_t)K, p.pos);
+    // chunk statistics of every row, then each chunk normalized with its row's merged statistics
+    const uint64_t chunks = ((uint64_t)p.pos + 1 + kSoftmaxChunk - 1) / kSoftmaxChunk;
+    BOOT_REQUIRE(groups <= 65535, "attention_softmax serves at most 65535 rows");
+    float2 *stats = (float2 *)context_workspace(c, groups * chunks * sizeof(float2));
+    BOOT_REQUIRE(stats, "cannot allocate softmax workspace");
+    const dim3 sgrid((uint32_t)chunks, (uint32_t)groups);
+    launch_timed(c, "softmax_stats_kernel", softmax_stats_kernel, sgrid, dim3(256), (const float *)b[0].ptr, stats,
+                 (uint32_t)K, p.pos, (uint32_t)chunks);
+    launch_timed(c, "softmax_apply_kernel", softmax_apply_kernel, sgrid, dim3(256), (float *)b[0].ptr,
+                 (const float2 *)stats, (uint32_t)K, p.pos, (uint32_t)chunks);
     return nullptr;
 }
 
@@ -887,10 +1069,32 @@ const char *launch_values_int8(Context &c, const View *b, int count, const boot_
     BOOT_REQUIRE(b[2].bytes >= rows * 16384 && b[3].bytes >= rows * 16384, "gate/output smaller than rows*4096 floats");
     BOOT_REQUIRE(b[4].bytes >= length * 8, "V scale buffer smaller than the attended length");
     BOOT_REQUIRE(aligned(b[1].ptr, 16), "V cache binding must be 16-byte aligned");
-    const uint64_t threads = rows * 4096;
-    values_int8_kernel<<<(uint32_t)((threads + 255) / 256), 256, 0, context_stream(c)>>>(
-        (const float *)b[0].ptr, (const int8_t *)b[1].ptr, (const float *)b[2].ptr, (float *)b[3].ptr,
-        (const float *)b[4].ptr, (uint32_t)rows, (uint32_t)K, p.pos);
+    // split partials over absolute kValuesSplit-token ranges, then their sum in order with the gate
+    const uint64_t splits = (K + kValuesSplit - 1) / kValuesSplit;
+    float *part = (float *)context_workspace(c, rows * 2 * splits * 2048 * sizeof(float));
+    BOOT_REQUIRE(part, "cannot allocate values workspace");
+    // rows per work-group: the fewest of 1, 2, 4, 8 that hold the dispatch's rows (fewer registers
+    // and more work-groups per CU for small verify blocks); a row's result is the same in each
+    const int per = rows >= 5 ? 8 : rows >= 3 ? 4 : rows == 2 ? 2 : 1;
+    const uint64_t zs = (rows + per - 1) / per;
+    BOOT_REQUIRE(zs <= 65535, "batch_attention_values_int8 serves at most 524280 rows");
+    const dim3 vgrid((uint32_t)splits, 2, (uint32_t)zs);
+    const float *sc = (const float *)b[0].ptr, *vsc = (const float *)b[4].ptr;
+    const int8_t *vc = (const int8_t *)b[1].ptr;
+    if (per == 8)
+        launch_timed(c, "values_partial_kernel", values_partial_kernel<8>, vgrid, dim3(256), sc, vc, vsc, part,
+                     (uint32_t)rows, (uint32_t)K, p.pos, (uint32_t)splits);
+    else if (per == 4)
+        launch_timed(c, "values_partial_kernel", values_partial_kernel<4>, vgrid, dim3(256), sc, vc, vsc, part,
+                     (uint32_t)rows, (uint32_t)K, p.pos, (uint32_t)splits);
+    else if (per == 2)
+        launch_timed(c, "values_partial_kernel", values_partial_kernel<2>, vgrid, dim3(256), sc, vc, vsc, part,
+                     (uint32_t)rows, (uint32_t)K, p.pos, (uint32_t)splits);
+    else
+        launch_timed(c, "values_partial_kernel", values_partial_kernel<1>, vgrid, dim3(256), sc, vc, vsc, part,
+                     (uint32_t)rows, (uint32_t)K, p.pos, (uint32_t)splits);
+    launch_timed(c, "values_combine_kernel", values_combine_kernel, dim3(16, (uint32_t)rows), dim3(256),
+                 (const float *)part, (const float *)b[2].ptr, (float *)b[3].ptr, (uint32_t)splits);
     return nullptr;
 }
 
