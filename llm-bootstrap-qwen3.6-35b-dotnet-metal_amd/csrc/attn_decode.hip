@@ -29,40 +29,100 @@ namespace {
 
 // ---------------------------------------------------------------- reference-compatible reader
 
-// scores[(row*16+h)*K + t] = (q . code) * ks[t*2+h/8] * (1/16), -inf beyond row's
-// causal end (kernels.metal:147-152). One thread per token, eight heads of one
-// KV group per block.
-__global__ __launch_bounds__(64) void scores_int8_kernel(const float *__restrict__ q, const int8_t *__restrict__ k,
-                                                         float *__restrict__ scores, const float *__restrict__ ks,
-                                                         uint32_t rows, uint32_t K, uint32_t pos) {
-    __shared__ float qs[8][256];
-    const uint32_t row = blockIdx.y >> 1, g = blockIdx.y & 1;
-    if (row >= rows) return;
-    for (int i = threadIdx.x; i < 8 * 256; i += 64) qs[i / 256][i % 256] = q[(size_t)row * 4096 + (g * 8) * 256 + i];
+// scores[(row*16+h)*K + t] = (q . code) * ks[t*2+h/8] * (1/16), -inf beyond row's causal end
+// (kernels.metal:147-152), on INT8 MFMA (v_mfma_i32_16x16x64_i8). Each (row, head) query is split
+// into three INT8 parts, q ~= s_q (q1 + q2 / 254 + q3 / 254^2) with s_q = max|q| / 127 (error
+// <= 6.1e-8 max|q| per element), the dot products with the codes are exact integers, and their
+// combination is FP32 per element: a row's scores do not depend on the rows it is dispatched
+// with. Work-group (256 tokens, KV group, kRows rows): the query operands of its rows in LDS
+// (16 columns: 8 heads x {q1, q2}, and 8 heads x q3 twice), wave w takes tokens 64w .. 64w + 63
+// in 16-token tiles; each K operand (16 bytes of a token's row per lane) feeds 2 kRows MFMAs.
+template <int kRows>
+__global__ __launch_bounds__(256) void scores_int8_kernel(const float *__restrict__ q, const int8_t *__restrict__ k,
+                                                          float *__restrict__ scores, const float *__restrict__ ks,
+                                                          uint32_t rows, uint32_t K, uint32_t pos) {
+    typedef int v4i __attribute__((ext_vector_type(4)));
+    __shared__ v4i qop[kRows][2][4][64];   // [row][set][64-dimension step][lane]
+    __shared__ float qscale[kRows][8];
+    const uint32_t g = blockIdx.y, r0 = blockIdx.z * kRows;
+    const uint32_t nr = min((uint32_t)kRows, rows - r0);
+    const uint32_t length = min(pos + rows, K);   // the cache rows read (validated by the launcher)
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n = lane & 15, qq = lane >> 4;
+    // ---- query parts: thread T takes head T / 32, dimensions 8 (T % 32) .. + 7 of each row
+    {
+        const int h = tid >> 5, d0 = 8 * (tid & 31);
+        auto code = [](float x) { return (uint32_t)(uint8_t)(int8_t)(int)fminf(fmaxf(x, -127.0f), 127.0f); };
+#pragma unroll
+        for (int r = 0; r < kRows; r++) {
+            float x[8];
+            const float *src = q + (size_t)(r0 + min((uint32_t)r, nr - 1)) * 4096 + (g * 8 + h) * 256 + d0;
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[e] = src[e];   // (the query binding needs only 4-byte alignment)
+            float amax = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(x[e]));
+#pragma unroll
+            for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));   // the head's 32 lanes
+            const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+            if ((tid & 31) == 0) qscale[r][h] = amax * (1.0f / 127.0f);
+            uint32_t w1[2] = {0, 0}, w2[2] = {0, 0}, w3[2] = {0, 0};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float z = x[e] * inv, q1 = rintf(z), r1 = z - q1;
+                const float q2 = rintf(r1 * 254.0f);
+                const float r2 = fmaf(r1, 254.0f, -q2);
+                const float q3 = rintf(r2 * 254.0f);
+                w1[e >> 2] |= code(q1) << (8 * (e & 3));
+                w2[e >> 2] |= code(q2) << (8 * (e & 3));
+                w3[e >> 2] |= code(q3) << (8 * (e & 3));
+            }
+            // dimension d0 + e is byte (d0 % 16) + e of lane 16 ((d0 % 64) / 16) + column of step d0 / 64
+            const int step = d0 >> 6, at = 16 * ((d0 & 63) >> 4), half = (d0 & 15) >> 3;
+            unsigned char *base = reinterpret_cast<unsigned char *>(&qop[r][0][step][0]);
+            *reinterpret_cast<uint2 *>(base + (at + h) * 16 + 8 * half) = make_uint2(w1[0], w1[1]);
+            *reinterpret_cast<uint2 *>(base + (at + h + 8) * 16 + 8 * half) = make_uint2(w2[0], w2[1]);
+            unsigned char *base3 = reinterpret_cast<unsigned char *>(&qop[r][1][step][0]);
+            *reinterpret_cast<uint2 *>(base3 + (at + h) * 16 + 8 * half) = make_uint2(w3[0], w3[1]);
+            *reinterpret_cast<uint2 *>(base3 + (at + h + 8) * 16 + 8 * half) = make_uint2(w3[0], w3[1]);
+        }
+    }
     __syncthreads();
-    const uint32_t t = blockIdx.x * 64 + threadIdx.x;
-    if (t >= K) return;
-    float acc[8];
-    const bool visible = t <= pos + row;
-    if (visible) {
+    const bool lo_col = n >= 8;
+#pragma unroll 1
+    for (int tile = 0; tile < 4; tile++) {
+        const uint32_t tb = blockIdx.x * 256 + 64 * wave + 16 * tile;
+        if (tb >= K) break;   // wave-uniform
+        const uint32_t tk = min(tb + n, length - 1);   // the lane's K row (an existing one)
+        v4i kop[4];
 #pragma unroll
-        for (int h = 0; h < 8; h++) acc[h] = 0.0f;
-        const int8_t *kr = k + ((size_t)t * 2 + g) * 256;
-        for (int d0 = 0; d0 < 256; d0 += 16) {
-            const uint4 w = *reinterpret_cast<const uint4 *>(kr + d0);
-            const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+        for (int jj = 0; jj < 4; jj++)
+            kop[jj] = *reinterpret_cast<const v4i *>(k + ((size_t)tk * 2 + g) * 256 + 64 * jj + 16 * qq);
+        float kss[4];
 #pragma unroll
-            for (int j = 0; j < 16; j++) {
-                const float code = (float)(int8_t)((words[j >> 2] >> (8 * (j & 3))) & 0xff);
+        for (int i = 0; i < 4; i++) kss[i] = ks[(size_t)min(tb + 4 * qq + i, length - 1) * 2 + g];
 #pragma unroll
-                for (int h = 0; h < 8; h++) acc[h] = fmaf(qs[h][d0 + j], code, acc[h]);
+        for (int r = 0; r < kRows; r++) {
+            if ((uint32_t)r >= nr) break;   // uniform
+            v4i acc = {0, 0, 0, 0}, acc3 = {0, 0, 0, 0};
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop[jj], qop[r][0][jj][lane], acc, 0, 0, 0);
+                acc3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop[jj], qop[r][1][jj][lane], acc3, 0, 0, 0);
+            }
+            // token tb + 4qq + i, column n; the partner column n ^ 8 holds the other part of the head
+            const float qsc = qscale[r][n & 7];
+            const uint32_t last = pos + r0 + r;   // the row's last visible key
+            float *dst = scores + ((size_t)(r0 + r) * 16 + g * 8 + (n & 7)) * K;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int mine = acc[i], other = __shfl_xor(mine, 8, 64);
+                const float hi = (float)(lo_col ? other : mine), lo = (float)(lo_col ? mine : other);
+                const float full = fmaf((float)acc3[i], 1.0f / 64516.0f, fmaf(lo, 1.0f / 254.0f, hi)) * qsc;
+                const uint32_t t = tb + 4 * qq + i;
+                if (!lo_col && t < K) dst[t] = t <= last ? full * kss[i] * (1.0f / 16.0f) : -INFINITY;
             }
         }
     }
-    const float scale = visible ? ks[(size_t)t * 2 + g] : 0.0f;
-#pragma unroll
-    for (int h = 0; h < 8; h++)
-        scores[((size_t)row * 16 + g * 8 + h) * K + t] = visible ? acc[h] * scale * (1.0f / 16.0f) : -INFINITY;
 }
 
 __device__ inline float block_reduce_256(float v, float *partial, bool is_max) {
@@ -1028,10 +1088,25 @@ const char *launch_scores_int8(Context &c, const View *b, int count, const boot_
     BOOT_REQUIRE(b[3].bytes >= length * 8, "K scale buffer smaller than the attended length");
     BOOT_REQUIRE(aligned(b[0].ptr, 4) && aligned(b[1].ptr, 16) && aligned(b[2].ptr, 4) && aligned(b[3].ptr, 4),
                  "bindings misaligned");
-    dim3 grid((uint32_t)((K + 63) / 64), (uint32_t)(rows * 2));
-    scores_int8_kernel<<<grid, 64, 0, context_stream(c)>>>((const float *)b[0].ptr, (const int8_t *)b[1].ptr,
-                                                           (float *)b[2].ptr, (const float *)b[3].ptr, (uint32_t)rows,
-                                                           (uint32_t)K, p.pos);
+    const int per = rows >= 5 ? 8 : rows >= 3 ? 4 : rows == 2 ? 2 : 1;
+    const uint64_t zs = (rows + per - 1) / per;
+    BOOT_REQUIRE(zs <= 65535, "batch_attention_scores_int8 serves at most 524280 rows");
+    const dim3 sgrid((uint32_t)((K + 255) / 256), 2, (uint32_t)zs);
+    const float *qp = (const float *)b[0].ptr, *ksp = (const float *)b[3].ptr;
+    const int8_t *kp = (const int8_t *)b[1].ptr;
+    float *sp = (float *)b[2].ptr;
+    if (per == 8)
+        launch_timed(c, "scores_int8_kernel", scores_int8_kernel<8>, sgrid, dim3(256), qp, kp, sp, ksp, (uint32_t)rows,
+                     (uint32_t)K, p.pos);
+    else if (per == 4)
+        launch_timed(c, "scores_int8_kernel", scores_int8_kernel<4>, sgrid, dim3(256), qp, kp, sp, ksp, (uint32_t)rows,
+                     (uint32_t)K, p.pos);
+    else if (per == 2)
+        launch_timed(c, "scores_int8_kernel", scores_int8_kernel<2>, sgrid, dim3(256), qp, kp, sp, ksp, (uint32_t)rows,
+                     (uint32_t)K, p.pos);
+    else
+        launch_timed(c, "scores_int8_kernel", scores_int8_kernel<1>, sgrid, dim3(256), qp, kp, sp, ksp, (uint32_t)rows,
+                     (uint32_t)K, p.pos);
     return nullptr;
 }
 

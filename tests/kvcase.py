@@ -70,3 +70,35 @@ def upload(device, array: np.ndarray, extra_bytes: int = 0):
 def rel_l2(got, ref):
     ref = np.asarray(ref, np.float64)
     return float(np.linalg.norm(np.asarray(got, np.float64) - ref) / max(np.linalg.norm(ref), 1e-300))
+
+
+def fp32_reader(q, kc, vc, ks, vs, gate, rows: int, history: int) -> np.ndarray:
+    """The reference's scalar reader in float32 arithmetic on the CPU, with its order of
+    accumulation (kernels.metal:147-166): each score's dot product summed over the dimensions in
+    order, times ks / 16; the softmax's sum as 256 strided per-thread sums (one threadgroup of 256
+    per row and head) then combined; each output summed over the keys in order, p * vs * code,
+    times sigmoid(gate). A float32 baseline for the GPU paths' rounding (NumPy reduces along a
+    leading axis element by element in order)."""
+    length = history + rows
+    codes_k = kc.reshape(-1, 2, 256)[:length].astype(np.float32)
+    pages = (length + 255) // 256
+    codes_v = vc[:pages * 2 * 65536].reshape(pages, 2, 256, 256).transpose(0, 3, 1, 2).reshape(pages * 256, 2, 256)
+    codes_v = codes_v[:length].astype(np.float32)
+    ks2, vs2 = ks.reshape(-1, 2)[:length], vs.reshape(-1, 2)[:length]
+    q3, g3 = q.reshape(rows, 16, 256).astype(np.float32), gate.reshape(rows, 16, 256).astype(np.float32)
+    kt = [np.ascontiguousarray(codes_k[:, kv].T) for kv in range(2)]   # [256 dims][keys]
+    y = np.empty((rows, 16, 256), np.float32)
+    for r in range(rows):
+        end = history + r + 1
+        for h in range(16):
+            kv = h // 8
+            dots = (kt[kv][:, :end] * q3[r, h][:, None]).sum(axis=0, dtype=np.float32)
+            s = dots * ks2[:end, kv] * np.float32(1.0 / 16.0)
+            e = np.exp(s - s.max(), dtype=np.float32)
+            padded = np.zeros(((end + 255) // 256) * 256, np.float32)
+            padded[:end] = e
+            total = padded.reshape(-1, 256).sum(axis=0, dtype=np.float32).sum(dtype=np.float32)
+            w = (e / total) * vs2[:end, kv]
+            o = (codes_v[:end, kv] * w[:, None]).sum(axis=0, dtype=np.float32)
+            y[r, h] = o * (np.float32(1.0) / (np.float32(1.0) + np.exp(-g3[r, h], dtype=np.float32)))
+    return y.ravel()
