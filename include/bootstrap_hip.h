@@ -101,12 +101,14 @@ int boot_read(void *ctx, void *buf, uint64_t offset, void *host, uint64_t bytes)
  * (tight serving loops, harnesses that forbid hipMalloc). ----
  *
  * boot_dispatch with the same arguments and outputs, except that kernels whose launch needs
- * split-K scratch (attention_decode_int8, attention_decode_append_int8, the attention_online_*
- * prefill names) draw it from a static 72 MiB device array of the library instead of the context
- * workspace; it calls no hipMalloc/hipFree or other allocating routine and records no timing
- * sample. Requests larger than 72 MiB are rejected (0, with the size in boot_error) before any
- * launch; 72 MiB covers prefill chunks of up to 512 rows and of 2048 rows on 256 CUs, and
- * single-token decode up to the 262144 window. One GPU has one array: the first split-K call of a command claims it
+ * scratch (split-K partials of attention_decode_int8, attention_decode_append_int8, the
+ * attention_online_* prefill names and batch_attention_values_int8; the chunk statistics of
+ * attention_softmax) draw it from a static 72 MiB device array of the library instead of the
+ * context workspace; it calls no hipMalloc/hipFree or other allocating routine and records no
+ * timing sample. Requests larger than 72 MiB are rejected (0, with the size in boot_error) before
+ * any launch; 72 MiB covers prefill chunks of up to 512 rows and of 2048 rows on 256 CUs,
+ * single-token decode up to the 262144 window, and the scalar reader for 8 rows up to 262144
+ * keys (values partials: rows x 2 x keys / 512 x 8 KiB, 64 MiB there). One GPU has one array: the first split-K call of a command claims it
  * for that context until the command's boot_end, and a split-K call of another context meanwhile
  * fails (0, "held by another context's command") instead of racing; calls in one context's
  * command are ordered on its stream. The context's stream is the library's own and boot_end

@@ -1,6 +1,7 @@
 """boot_dispatch_noalloc (the entry point that allocates nothing) against boot_dispatch on the
-same inputs: split-K decode and prefill on a fresh context, the no-allocation calls first (before
-the context has any workspace) with boot_allocated unchanged across each of them, two calls in a
+same inputs: split-K decode, prefill and the scalar reader on a fresh context, the no-allocation
+calls first (before the context has any workspace) with boot_allocated unchanged across each of
+them, two calls in a
 row with the second smaller, results bitwise equal and within the FP64 bar; sizes beyond the
 static scratch are refused, and so is a second context's split-K call while the first context's
 command holds the scratch."""
@@ -58,14 +59,42 @@ def prefill(device, q, gate, cache, rows, history, noalloc):
     return y[:-1]
 
 
+def reader(device, q, gate, cache, rows, history, noalloc):
+    """The scalar reader of a verify block (batch_attention_scores_int8, attention_softmax,
+    batch_attention_values_int8), whose softmax statistics and values partials are scratch."""
+    qb, gb = upload(device, q), upload(device, gate)
+    length = history + rows
+    scores = device.allocate(rows * 16 * length * 4)
+    out = device.allocate(q.nbytes + 4)
+    out.write(np.full(rows * 4096 + 1, np.nan, np.float32))
+    p = KernelArgs(M=rows, K=length, Position=history)
+    before = device.allocated_bytes
+    device.begin()
+    device.dispatch2d("batch_attention_scores_int8", p, length * 32, rows * 16, 128, qb, cache.kc, scores, cache.ks,
+                      noalloc=noalloc)
+    device.dispatch("attention_softmax", KernelArgs(M=rows, K=length, Position=length - 1), rows * 16 * 256, 256,
+                    scores, noalloc=noalloc)
+    device.dispatch("batch_attention_values_int8", p, rows * 4096, 128, scores, cache.vc, gb, out, cache.vs,
+                    noalloc=noalloc)
+    device.end()
+    if noalloc:
+        assert device.allocated_bytes == before, "boot_dispatch_noalloc allocated device memory"
+    y = out.read(np.float32, rows * 4096 + 1)
+    for b in (qb, gb, scores, out):
+        b.dispose()
+    assert np.isnan(y[-1])
+    return y[:-1]
+
+
 @pytest.mark.parametrize("kind,cases", [
     ("decode", [(131071, 1), (4093, 7)]),        # 114 splits per group, then 6
     ("prefill", [(30208, 512), (257, 33)]),      # 68 MB of partial slots, then a 33-row chunk (decode kernel, 3 splits)
+    ("reader", [(65528, 8), (4093, 3)]),         # 16 MB of values partials and 8-row softmax statistics, then 3 rows
 ])
 def test_noalloc_matches_dispatch(oracle, kind, cases):
     """A fresh context: every no-allocation call runs before the context has a workspace, so a
     path that fell back to (or grew) the workspace would show in boot_allocated."""
-    run = decode if kind == "decode" else prefill
+    run = {"decode": decode, "prefill": prefill, "reader": reader}[kind]
     with Device() as device:
         prepared = []
         for history, rows in cases:
