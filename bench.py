@@ -348,6 +348,47 @@ def cpu_baseline(work: "PrefillWorkload", dec: "DecodeWorkload", y_last, runs: i
             "entries": entries}, parity
 
 
+# --------------------------------------------------------------------------- verify reader
+
+def verify_reader(dec, rows: int = 8, runs: int = 5):
+    """The scalar reader a speculative verify block runs (Prefill.cs:269-285, kernels.metal:147-166:
+    batch_attention_scores_int8, attention_softmax, batch_attention_values_int8) for `rows` draft
+    rows at the end of config 4's cache (layer 0), kernel-exact, mean of `runs` blocks."""
+    d = dec.device
+    layer = dec.cache.layers[0]
+    length = dec.pos0 + dec.steps
+    history = length - rows
+    scores = d.allocate(rows * 16 * length * 4)
+    out = d.allocate(rows * 16384)
+    p = KernelArgs(M=rows, K=length, Position=history)
+
+    def block():
+        d.dispatch2d("batch_attention_scores_int8", p, length * 32, rows * 16, 128, dec.q, layer.key, scores,
+                     layer.key_scale)
+        d.dispatch("attention_softmax", KernelArgs(M=rows, K=length, Position=length - 1), rows * 16 * 256, 256, scores)
+        d.dispatch("batch_attention_values_int8", p, rows * 4096, 128, scores, layer.value, dec.gate, out,
+                   layer.value_scale)
+
+    d.begin()
+    block()
+    d.end()
+    d.reset_wall_timing(kernels_exact=True)
+    d.begin()
+    for _ in range(runs):
+        block()
+    d.end()
+    names = ["scores_int8_kernel", "softmax_stats_kernel", "softmax_apply_kernel", "values_partial_kernel",
+             "values_combine_kernel"]
+    ks = kernel_stats(d, names)
+    us = {n: round(ks[n][0] / runs * 1000, 2) for n in names if n in ks}
+    for b in (scores, out):
+        b.dispose()
+    return {"history": history, "rows": rows, "kernel_us": us, "total_us": round(sum(us.values()), 2),
+            "kv_bytes": 1040 * length,
+            "what": "scores (INT8 MFMA, three-part query), softmax (chunk statistics, then normalize), values "
+                    "(split-K FP16 MFMA, then the splits' sum with the gate), kernel-exact, one layer"}
+
+
 # --------------------------------------------------------------------------- decode
 
 class DecodeWorkload:
@@ -562,6 +603,9 @@ def main():
             "frac": round(bulk_bytes / (bulk * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic("kv_store_int8 bulk 131072"),
             "bytes": bulk_bytes, "kernel_ms": round(bulk, 4)}
+    if dec is not None:
+        log("verify reader: 8 rows at the end of config 4's cache")
+        result["verify_reader"] = verify_reader(dec)
     if not args.no_cpu_baseline:
         log("cpu baseline: the FP64 checker on configs 1, 2, a 131072 decode step and config 3's last chunk")
         result["cpu_baseline"], result["parity_last_chunk"] = cpu_baseline(work, dec, y_int8)
