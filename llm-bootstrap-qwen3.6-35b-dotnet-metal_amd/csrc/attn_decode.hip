@@ -1088,17 +1088,17 @@ const char *launch_scores_int8(Context &c, const View *b, int count, const boot_
     BOOT_REQUIRE(b[3].bytes >= length * 8, "K scale buffer smaller than the attended length");
     BOOT_REQUIRE(aligned(b[0].ptr, 4) && aligned(b[1].ptr, 16) && aligned(b[2].ptr, 4) && aligned(b[3].ptr, 4),
                  "bindings misaligned");
-    const int per = rows >= 5 ? 8 : rows >= 3 ? 4 : rows == 2 ? 2 : 1;
+    // rows per work-group: the fewest of 1, 2, 4 that hold the dispatch's rows, at most 4 (an
+    // 8-row work-group reads K once for all rows but holds one work-group per CU and streams
+    // slower: 63.6 against 54.0 us at 8 rows over 131072 keys); a row's scores are the same in each
+    const int per = rows >= 3 ? 4 : rows == 2 ? 2 : 1;
     const uint64_t zs = (rows + per - 1) / per;
-    BOOT_REQUIRE(zs <= 65535, "batch_attention_scores_int8 serves at most 524280 rows");
+    BOOT_REQUIRE(zs <= 65535, "batch_attention_scores_int8 serves at most 262140 rows");
     const dim3 sgrid((uint32_t)((K + 255) / 256), 2, (uint32_t)zs);
     const float *qp = (const float *)b[0].ptr, *ksp = (const float *)b[3].ptr;
     const int8_t *kp = (const int8_t *)b[1].ptr;
     float *sp = (float *)b[2].ptr;
-    if (per == 8)
-        launch_timed(c, "scores_int8_kernel", scores_int8_kernel<8>, sgrid, dim3(256), qp, kp, sp, ksp, (uint32_t)rows,
-                     (uint32_t)K, p.pos);
-    else if (per == 4)
+    if (per == 4)
         launch_timed(c, "scores_int8_kernel", scores_int8_kernel<4>, sgrid, dim3(256), qp, kp, sp, ksp, (uint32_t)rows,
                      (uint32_t)K, p.pos);
     else if (per == 2)
@@ -1148,18 +1148,16 @@ const char *launch_values_int8(Context &c, const View *b, int count, const boot_
     const uint64_t splits = (K + kValuesSplit - 1) / kValuesSplit;
     float *part = (float *)context_workspace(c, rows * 2 * splits * 2048 * sizeof(float));
     BOOT_REQUIRE(part, "cannot allocate values workspace");
-    // rows per work-group: the fewest of 1, 2, 4, 8 that hold the dispatch's rows (fewer registers
-    // and more work-groups per CU for small verify blocks); a row's result is the same in each
-    const int per = rows >= 5 ? 8 : rows >= 3 ? 4 : rows == 2 ? 2 : 1;
+    // rows per work-group: the fewest of 1, 2, 4 that hold the dispatch's rows, at most 4 (8 rows
+    // take 276 registers, one work-group per CU: 74.0 against 52.2 us at 8 rows over 131072 keys;
+    // 2 rows read V four times: 63.6 us); a row's result is the same in each
+    const int per = rows >= 3 ? 4 : rows == 2 ? 2 : 1;
     const uint64_t zs = (rows + per - 1) / per;
-    BOOT_REQUIRE(zs <= 65535, "batch_attention_values_int8 serves at most 524280 rows");
+    BOOT_REQUIRE(zs <= 65535, "batch_attention_values_int8 serves at most 262140 rows");
     const dim3 vgrid((uint32_t)splits, 2, (uint32_t)zs);
     const float *sc = (const float *)b[0].ptr, *vsc = (const float *)b[4].ptr;
     const int8_t *vc = (const int8_t *)b[1].ptr;
-    if (per == 8)
-        launch_timed(c, "values_partial_kernel", values_partial_kernel<8>, vgrid, dim3(256), sc, vc, vsc, part,
-                     (uint32_t)rows, (uint32_t)K, p.pos, (uint32_t)splits);
-    else if (per == 4)
+    if (per == 4)
         launch_timed(c, "values_partial_kernel", values_partial_kernel<4>, vgrid, dim3(256), sc, vc, vsc, part,
                      (uint32_t)rows, (uint32_t)K, p.pos, (uint32_t)splits);
     else if (per == 2)
