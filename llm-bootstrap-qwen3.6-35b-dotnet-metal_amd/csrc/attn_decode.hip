@@ -958,117 +958,71 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
     }
 }
 
-// Merges the splits of one (row, head) for 64 dimensions (grid: 4 dimension
-// chunks x 16 heads x rows). Thread s loads m_s and l_s of every split at once (the
-// block maximum, the weights exp2(m_s - max) into LDS and the weighted sum of l);
-// 4 groups of 64 lanes take the float4 partials of every 4th split, the first 128
-// splits' partials loaded together with m and l since they do not depend on the
-// weights, and the groups are added in LDS.
+// Merges the splits of one (row, head) (grid: 4 x 16 heads x rows, four waves per work-group).
+// Each wave owns 16 dimensions and works alone (no LDS, no barrier): lane (sg, q) holds the
+// float4 of dimensions 4q .. 4q + 3 for splits sg, sg + 16, ... (the first 128 splits' m, l and
+// partials loaded at once), the maximum of m and then the weighted sums of l and O are reduced
+// over the 16 split groups, and the lanes of group 0 write the output. The order of every sum
+// is fixed by the split count alone.
 __global__ __launch_bounds__(256) void decode_combine_kernel(const float *__restrict__ partial, const float *__restrict__ gate,
                                                              float *__restrict__ y, uint32_t splits) {
-    __shared__ float weight[kMaxDecodeSplits];
-    __shared__ float red[4], lred[4];
-    __shared__ float4 sums[4][16];
     const uint32_t row = blockIdx.z, hq = blockIdx.y, g = hq / 8, h = hq % 8;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int q = lane & 3, sg = lane >> 2;
+    const uint32_t d = (blockIdx.x * 4 + wave) * 16 + 4 * q;
     const float *base = partial + ((size_t)row * 2 + g) * splits * kPartialFloats;
-    constexpr int kPer = kMaxDecodeSplits / 256;
-    float ms[kPer], ls[kPer];
-#pragma unroll
-    for (int i = 0; i < kPer; i++) {
-        const uint32_t sidx = min((uint32_t)(tid + 256 * i), splits - 1);
-        ms[i] = tid + 256 * i < (int)splits ? base[(size_t)sidx * kPartialFloats + 2048 + h] : -INFINITY;
-        ls[i] = base[(size_t)sidx * kPartialFloats + 2056 + h];
-    }
-    // group `wave` takes splits wave, wave + 4, ...; lane: 4 dims of the 64-dim chunk,
-    // sub-lane `sub` the splits wave + 4 sub + 16 u
-    const uint32_t d = blockIdx.x * 64 + 4 * (lane & 15);
-    const int sub = lane >> 4;
-    const float *col = base + (size_t)h * 256 + d;
     constexpr int kEarly = 8;
-    float4 pv[kEarly];
+    float mv[kEarly], lv[kEarly];
+    float4 ov[kEarly];
 #pragma unroll
     for (int u = 0; u < kEarly; u++) {
-        const uint32_t sidx = min((uint32_t)(wave + 4 * sub + 16 * u), splits - 1);
-        pv[u] = *reinterpret_cast<const float4 *>(col + (size_t)sidx * kPartialFloats);
+        const uint32_t s = sg + 16 * u, sidx = min(s, splits - 1);
+        const float *sp = base + (size_t)sidx * kPartialFloats;
+        ov[u] = *reinterpret_cast<const float4 *>(sp + h * 256 + d);
+        mv[u] = s < splits ? sp[2048 + h] : -INFINITY;
+        lv[u] = sp[2056 + h];
     }
-    const size_t at = ((size_t)row * 16 + hq) * 256 + blockIdx.x * 64 + 4 * (tid & 15);
+    const size_t at = ((size_t)row * 16 + hq) * 256 + d;
     float gv[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) gv[i] = gate[at + i];   // y and gate need only 4-byte alignment
-    float mmax = -INFINITY;
+    float mmax = mv[0];
 #pragma unroll
-    for (int i = 0; i < kPer; i++) mmax = fmaxf(mmax, ms[i]);
+    for (int u = 1; u < kEarly; u++) mmax = fmaxf(mmax, mv[u]);
+    for (uint32_t s = sg + 16 * kEarly; s < splits; s += 16) mmax = fmaxf(mmax, base[(size_t)s * kPartialFloats + 2048 + h]);
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, o, 64));
-    if (lane == 0) red[wave] = mmax;
-    __syncthreads();
-    mmax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int o = 4; o < 64; o <<= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, o, 64));
     float lsum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kPer; i++) {
-        if (tid + 256 * i >= (int)splits) continue;
-        const float w = ms[i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms[i] - mmax);
-        weight[tid + 256 * i] = w;
-        lsum += ls[i] * w;
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o, 64);
-    if (lane == 0) lred[wave] = lsum;
-    __syncthreads();
-    lsum = (lred[0] + lred[1]) + (lred[2] + lred[3]);
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    auto add = [&](float m, float l, const float4 &o) {
+        if (m == -INFINITY) return;   // a split that holds none of the row's keys
+        const float w = __builtin_amdgcn_exp2f(m - mmax);
+        lsum += l * w;
+        acc.x += o.x * w;
+        acc.y += o.y * w;
+        acc.z += o.z * w;
+        acc.w += o.w * w;
+    };
 #pragma unroll
-    for (int u = 0; u < kEarly; u++) {
-        const uint32_t sidx = wave + 4 * sub + 16 * u;
-        const float w = sidx < splits ? weight[sidx] : 0.0f;
-        acc.x += pv[u].x * w;
-        acc.y += pv[u].y * w;
-        acc.z += pv[u].z * w;
-        acc.w += pv[u].w * w;
+    for (int u = 0; u < kEarly; u++) add(mv[u], lv[u], ov[u]);
+    for (uint32_t s = sg + 16 * kEarly; s < splits; s += 16) {
+        const float *sp = base + (size_t)s * kPartialFloats;
+        add(sp[2048 + h], sp[2056 + h], *reinterpret_cast<const float4 *>(sp + h * 256 + d));
     }
-    for (uint32_t s0 = wave + 4 * sub + 16 * kEarly; s0 < splits; s0 += 64) {
-        float4 v[4];
-        float w[4];
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const uint32_t sidx = s0 + 16 * u;
-            const bool in = sidx < splits;
-            v[u] = *reinterpret_cast<const float4 *>(col + (size_t)min(sidx, splits - 1) * kPartialFloats);
-            w[u] = in ? weight[sidx] : 0.0f;
-        }
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            acc.x += v[u].x * w[u];
-            acc.y += v[u].y * w[u];
-            acc.z += v[u].z * w[u];
-            acc.w += v[u].w * w[u];
-        }
-    }
-    // the 16 (wave, sub) partial sums of each dim quad
-#pragma unroll
-    for (int o = 16; o < 64; o <<= 1) {
+    for (int o = 4; o < 64; o <<= 1) {
+        lsum += __shfl_xor(lsum, o, 64);
         acc.x += __shfl_xor(acc.x, o, 64);
         acc.y += __shfl_xor(acc.y, o, 64);
         acc.z += __shfl_xor(acc.z, o, 64);
         acc.w += __shfl_xor(acc.w, o, 64);
     }
-    if (sub == 0) sums[wave][lane] = acc;
-    __syncthreads();
-    if (tid < 16) {
-        float4 t = sums[0][tid];
-#pragma unroll
-        for (int w = 1; w < 4; w++) {
-            t.x += sums[w][tid].x;
-            t.y += sums[w][tid].y;
-            t.z += sums[w][tid].z;
-            t.w += sums[w][tid].w;
-        }
+    if (sg == 0) {
         const float inv = 1.0f / lsum;
-        y[at + 0] = t.x * inv * sigmoidf(gv[0]);
-        y[at + 1] = t.y * inv * sigmoidf(gv[1]);
-        y[at + 2] = t.z * inv * sigmoidf(gv[2]);
-        y[at + 3] = t.w * inv * sigmoidf(gv[3]);
+        y[at + 0] = acc.x * inv * sigmoidf(gv[0]);
+        y[at + 1] = acc.y * inv * sigmoidf(gv[1]);
+        y[at + 2] = acc.z * inv * sigmoidf(gv[2]);
+        y[at + 3] = acc.w * inv * sigmoidf(gv[3]);
     }
 }
 
