@@ -201,14 +201,17 @@ __global__ __launch_bounds__(256) void softmax_apply_kernel(float *__restrict__ 
 constexpr int kValuesSplit = 512;
 
 // Work-group (split, KV group, kRows rows): O^T[d][c] += V^T[d][t] B[t][c] on
-// v_mfma_f32_16x16x16_f16 with the codes exact in FP16 and, per row, B = p * vs / vs_r in the
-// 16 columns 8 heads x {FP16 hi, FP16 lo} (vs_r the row's largest V scale over its tokens of the
-// split, so that B <= 1; hi + lo keeps about 22 bits), the result times vs_r. Wave w takes
+// v_mfma_f32_16x16x16_f16 with the codes exact in FP16 and, per row, B = p * vs * 2^15 / vs_r in
+// the 16 columns 8 heads x {FP16 hi, FP16 lo} (vs_r the row's largest V scale over its tokens of
+// the split, so that B <= 2^15; hi + lo keeps about 22 bits), the result times vs_r / 2^15. The
+// factor 2^15 keeps the probabilities of a long, flat row (p ~ 1 / K) out of FP16's subnormals
+// (below 2^-14), where hi and lo would keep only a few bits. Wave w takes
 // dimensions 64w .. 64w + 63; a 64-token block is four k-steps, lane (n, qq) of step s holding
 // tokens 16qq + 4s .. + 3 of the block for both operands (one 16-byte code load per dimension
 // tile covers its four steps), and the next block's loads are issued before the current block is
 // staged. Every quantity of a row depends on that row's range only, whatever kRows is.
 constexpr int kVmBlock = 64;
+constexpr float kValuesScale = 32768.0f;   // 2^15: B's factor
 
 template <int kRows>
 __global__ __launch_bounds__(256) void values_partial_kernel(const float *__restrict__ scores,
@@ -288,7 +291,7 @@ __global__ __launch_bounds__(256) void values_partial_kernel(const float *__rest
             for (int i = 0; i < kEnt; i++) {
                 const int rh = pair0 + 4 * i, r = rh >> 3, h = rh & 7;
                 if ((uint32_t)r < nr) {
-                    const float inv = vr[r] > 0.0f ? 1.0f / vr[r] : 0.0f;
+                    const float inv = vr[r] > 0.0f ? kValuesScale / vr[r] : 0.0f;
                     const float x = cur.sc[i] * cur.sv * inv;
                     const _Float16 hi = (_Float16)x, lo = (_Float16)(x - (float)hi);
                     reinterpret_cast<_Float16 *>(&bs[r][s][lrow + h])[j] = hi;
@@ -323,13 +326,14 @@ __global__ __launch_bounds__(256) void values_partial_kernel(const float *__rest
     for (int r = 0; r < kRows; r++) {
         if ((uint32_t)r >= nr) break;
         float *out = partial + (((size_t)(r0 + r) * 2 + g) * splits + split) * 2048;
+        const float f = vr[r] * (1.0f / kValuesScale);   // exact: a power of two
 #pragma unroll
         for (int dt = 0; dt < 4; dt++) {
             float4 o4;
-            o4.x = (acc[dt][r][0] + __shfl_xor(acc[dt][r][0], 8, 64)) * vr[r];
-            o4.y = (acc[dt][r][1] + __shfl_xor(acc[dt][r][1], 8, 64)) * vr[r];
-            o4.z = (acc[dt][r][2] + __shfl_xor(acc[dt][r][2], 8, 64)) * vr[r];
-            o4.w = (acc[dt][r][3] + __shfl_xor(acc[dt][r][3], 8, 64)) * vr[r];
+            o4.x = (acc[dt][r][0] + __shfl_xor(acc[dt][r][0], 8, 64)) * f;
+            o4.y = (acc[dt][r][1] + __shfl_xor(acc[dt][r][1], 8, 64)) * f;
+            o4.z = (acc[dt][r][2] + __shfl_xor(acc[dt][r][2], 8, 64)) * f;
+            o4.w = (acc[dt][r][3] + __shfl_xor(acc[dt][r][3], 8, 64)) * f;
             if (n < 8) *reinterpret_cast<float4 *>(out + n * 256 + 64 * wave + 16 * dt + 4 * qq) = o4;
         }
     }

@@ -12,6 +12,9 @@
   Int8KvTests.cs:154-156.
 * prefill over heavy-tailed K/V (config 5's Student-t nu = 4): the re-append chunks at history
   200000 + 512c (c = 0, 15) and a 64-row block ending at the 262144-token window.
+* decode over the same heavy-tailed data, through the fused decode and through the three-dispatch
+  scalar reader (scores, softmax, values), at history 200000 (1 row) and ending at the window
+  (8 rows).
 * INT8 against FP16 KV storage on the same raw K/V (Int8KvTests.cs:138-150,189): the GPU
   outputs of both paths and the FP64 quantization error the reference reports
   (max_abs_quantization_vs_fp16), at config 3's last chunk and at the reference's (8192, 128).
@@ -24,7 +27,7 @@ import pytest
 
 from bootstrap_hip import Int8KvCache, KernelArgs, engine
 from bootstrap_hip import DeviceAttentionWorkspace, Fp16KvLayer, encode_online_fp16
-from kvcase import poison_tail, reference_kv, rel_l2, upload, upload_cache
+from kvcase import fp32_reader, poison_tail, reference_kv, rel_l2, upload, upload_cache
 
 pytestmark = pytest.mark.gpu
 
@@ -181,6 +184,59 @@ def test_prefill_heavy_tailed(device, oracle, history, rows):
     print(f"heavy-tailed prefill ({history},{rows}): rel-L2 {rel_l2(y, ref):.3e} max-abs {err.max():.3e}")
     assert rel_l2(y, ref) <= REL_L2 and err.max() <= MAX_ABS, (rel_l2(y, ref), err.max())
     assert np.all(err <= bound / 256 + 1e-4)           # Int8KvTests.cs:154-156
+    cache.dispose()
+
+
+def decode(device, q, gate, cache, rows, history, path):
+    qb, gb = upload(device, q), upload(device, gate)
+    out = device.allocate(rows * 16384 + 4)
+    out.write(np.full(rows * 4096 + 1, np.nan, np.float32))
+    length = history + rows
+    p = KernelArgs(M=rows, K=length, Position=history)
+    scores = None
+    device.begin()
+    if path == "fused":
+        device.dispatch("attention_decode_int8", p, rows * 4096, 256, qb, cache.kc, cache.vc, gb, out, cache.ks,
+                        cache.vs)
+    else:
+        scores = device.allocate(rows * 16 * length * 4)
+        device.dispatch2d("batch_attention_scores_int8", p, length * 32, rows * 16, 128, qb, cache.kc, scores,
+                          cache.ks)
+        device.dispatch("attention_softmax", KernelArgs(M=rows, K=length, Position=length - 1), rows * 16 * 256, 256,
+                        scores)
+        device.dispatch("batch_attention_values_int8", p, rows * 4096, 128, scores, cache.vc, gb, out, cache.vs)
+    device.end()
+    y = out.read(np.float32, rows * 4096 + 1)
+    for b in (qb, gb, out) + ((scores,) if scores is not None else ()):
+        b.dispose()
+    assert np.isnan(y[-1]), "output guard overwritten"
+    return y[:-1]
+
+
+@pytest.mark.parametrize("history,rows", [(200000, 1), (262136, 8)])
+def test_decode_heavy_tailed(device, oracle, history, rows):
+    """The fused decode (p * vs / vs_ref as FP16 hi + lo) and the scalar reader over Student-t
+    K/V, whose V scales vary widely within a split, against FP64 (the reference's FP32 query,
+    no FP16 rounding), with the per-element bound of Int8KvTests.cs:154-156."""
+    q, gate, host = heavy_case(oracle, history, rows, seed=800 + history % 1000)
+    cache = upload_cache(device, *host)
+    ref, bound = oracle.attention(q, *host, gate, rows, history, round_q_half=0, with_bound=True)
+    errors = {}
+    for path in ("fused", "reader"):
+        y = decode(device, q, gate, cache, rows, history, path)
+        assert np.all(np.isfinite(y))
+        err = np.abs(y - ref)
+        errors[path] = rel_l2(y, ref)
+        print(f"heavy-tailed decode {path} ({history},{rows}): rel-L2 {rel_l2(y, ref):.3e} max-abs {err.max():.3e}")
+        assert rel_l2(y, ref) <= REL_L2 and err.max() <= MAX_ABS, (path, rel_l2(y, ref), err.max())
+        assert np.all(err <= bound / 256 + 1e-4), path
+    if rows == 1:
+        # a long, flat row (p ~ 1 / 200000): both GPU paths as close to FP64 as the reference's
+        # reader evaluated in float32 (its probabilities then sit far below FP16's normal range)
+        e_fp32 = rel_l2(fp32_reader(q, *host, gate, rows, history), ref)
+        print(f"float32 reader: rel-L2 {e_fp32:.3e}")
+        for path, e in errors.items():
+            assert e <= 1.5 * e_fp32 + 1e-6, (path, e, e_fp32)
     cache.dispose()
 
 
