@@ -288,6 +288,33 @@ def test_decode_shape_sweep(device, oracle, history, rows):
     cache.dispose()
 
 
+@pytest.mark.parametrize("path", ["prefill", "fused", "reference"])
+def test_zero_value_run(device, oracle, path):
+    """A run of 2048 tokens whose V vectors are all zero (scale 0, codes 0: the quantizer's rule for
+    a zero vector, Int8KvTests.cs:60) covers whole key splits of the prefill, the fused decode and
+    the reader, so a split's largest V scale is 0: such a split adds its keys' weight to the
+    denominator and nothing to the output."""
+    history, rows = 8192, 33
+    k, v = reference_kv(history + rows)
+    v[1024:3072] = 0
+    q, gate, host = build_case(oracle, history, rows, kv=(k, v))
+    assert not host[3][1024 * 2:3072 * 2].any()
+    cache = upload_cache(device, *host)
+    if path == "prefill":
+        y = run_prefill(device, q, gate, cache, rows, history)
+        ref, bound = oracle.attention(q, *host, gate, rows, history, round_q_half=1, with_bound=True)
+    else:
+        y = run_decode(device, q, gate, cache, rows, history, path=path)
+        ref, bound = oracle.attention(q, *host, gate, rows, history, round_q_half=0, with_bound=True)
+    assert np.isnan(y[-1])
+    y = y[:-1]
+    assert np.all(np.isfinite(y))
+    err = np.abs(y - ref)
+    assert rel_l2(y, ref) <= REL_L2 and err.max() <= MAX_ABS, (rel_l2(y, ref), err.max())
+    assert np.all(err <= bound / 256 + 1e-4)
+    cache.dispose()
+
+
 @pytest.mark.parametrize("history,rows,spikes", [
     # a 131072-token context: 1152-token splits of nine 128-token chunks, spikes in later
     # chunks of the first split, mid-context and at the end
