@@ -113,13 +113,25 @@ __global__ __launch_bounds__(256) void scores_int8_kernel(const float *__restric
             const float qsc = qscale[r][n & 7];
             const uint32_t last = pos + r0 + r;   // the row's last visible key
             float *dst = scores + ((size_t)(r0 + r) * 16 + g * 8 + (n & 7)) * K;
+            float out[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int mine = acc[i], other = __shfl_xor(mine, 8, 64);
                 const float hi = (float)(lo_col ? other : mine), lo = (float)(lo_col ? mine : other);
                 const float full = fmaf((float)acc3[i], 1.0f / 64516.0f, fmaf(lo, 1.0f / 254.0f, hi)) * qsc;
                 const uint32_t t = tb + 4 * qq + i;
-                if (!lo_col && t < K) dst[t] = t <= last ? full * kss[i] * (1.0f / 16.0f) : -INFINITY;
+                out[i] = t <= last ? full * kss[i] * (1.0f / 16.0f) : -INFINITY;
+            }
+            // the lane's four consecutive tokens as one 16-byte store where the row allows it
+            const uint32_t t4 = tb + 4 * qq;
+            if (!lo_col) {
+                if (t4 + 3 < K && (reinterpret_cast<uintptr_t>(dst + t4) & 15) == 0) {
+                    *reinterpret_cast<float4 *>(dst + t4) = make_float4(out[0], out[1], out[2], out[3]);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        if (t4 + i < K) dst[t4 + i] = out[i];
+                }
             }
         }
     }
