@@ -165,12 +165,14 @@ __global__ __launch_bounds__(256) void softmax_stats_kernel(const float *__restr
     const uint32_t c = blockIdx.x, r = blockIdx.y;
     const float *row = x + (size_t)r * K;
     const uint32_t lo = c * kSoftmaxChunk, hi = min(pos + 1, lo + kSoftmaxChunk);
+    // every chunk holds at least one element at or below pos: loads of a clamped index, then the
+    // elements past the row's end are masked (no branch per load)
     float e[kSoftmaxPer];
 #pragma unroll
-    for (int j = 0; j < kSoftmaxPer; j++) {
-        const uint32_t i = lo + threadIdx.x + 256 * j;
-        e[j] = i < hi ? row[i] : -INFINITY;
-    }
+    for (int j = 0; j < kSoftmaxPer; j++) e[j] = row[min(lo + threadIdx.x + 256 * j, hi - 1)];
+#pragma unroll
+    for (int j = 0; j < kSoftmaxPer; j++)
+        if (lo + threadIdx.x + 256 * j >= hi) e[j] = -INFINITY;
     float top = -INFINITY;
 #pragma unroll
     for (int j = 0; j < kSoftmaxPer; j++) top = fmaxf(top, e[j]);
@@ -186,24 +188,28 @@ __global__ __launch_bounds__(256) void softmax_stats_kernel(const float *__restr
 __global__ __launch_bounds__(256) void softmax_apply_kernel(float *__restrict__ x, const float2 *__restrict__ stats,
                                                             uint32_t K, uint32_t pos, uint32_t chunks) {
     const uint32_t c = blockIdx.x, r = blockIdx.y;
+    // the chunk's loads go out first; the row's statistics (the same for the whole work-group)
+    // are merged while they are in flight
+    float *row = x + (size_t)r * K;
+    const uint32_t lo = c * kSoftmaxChunk, hi = min(pos + 1, lo + kSoftmaxChunk);
+    float e[kSoftmaxPer];
+#pragma unroll
+    for (int j = 0; j < kSoftmaxPer; j++) e[j] = row[min(lo + threadIdx.x + 256 * j, hi - 1)];
     const float2 *st = stats + (size_t)r * chunks;
     float top = -INFINITY;
     for (uint32_t k = 0; k < chunks; k++) top = fmaxf(top, st[k].x);
     float sum = 0.0f;
     for (uint32_t k = 0; k < chunks; k++)
         if (st[k].x != -INFINITY) sum += st[k].y * expf(st[k].x - top);
-    float *row = x + (size_t)r * K;
-    const uint32_t lo = c * kSoftmaxChunk, hi = min(pos + 1, lo + kSoftmaxChunk);
-    float e[kSoftmaxPer];
+    if (hi == lo + kSoftmaxChunk) {   // a whole chunk: no mask per store
 #pragma unroll
-    for (int j = 0; j < kSoftmaxPer; j++) {
-        const uint32_t i = lo + threadIdx.x + 256 * j;
-        e[j] = i < hi ? row[i] : 0.0f;
-    }
+        for (int j = 0; j < kSoftmaxPer; j++) row[lo + threadIdx.x + 256 * j] = expf(e[j] - top) / sum;
+    } else {
 #pragma unroll
-    for (int j = 0; j < kSoftmaxPer; j++) {
-        const uint32_t i = lo + threadIdx.x + 256 * j;
-        if (i < hi) row[i] = expf(e[j] - top) / sum;
+        for (int j = 0; j < kSoftmaxPer; j++) {
+            const uint32_t i = lo + threadIdx.x + 256 * j;
+            if (i < hi) row[i] = expf(e[j] - top) / sum;
+        }
     }
 }
 
@@ -351,21 +357,20 @@ __global__ __launch_bounds__(256) void values_partial_kernel(const float *__rest
     }
 }
 
-__global__ __launch_bounds__(256) void values_combine_kernel(const float *__restrict__ partial,
+__global__ __launch_bounds__(64) void values_combine_kernel(const float *__restrict__ partial,
                                                              const float *__restrict__ gate, float *__restrict__ y,
                                                              uint32_t splits) {
-    const uint32_t h = blockIdx.x, row = blockIdx.y, g = h / 8, d = threadIdx.x;
+    const uint32_t h = blockIdx.x / 4, row = blockIdx.y, g = h / 8, d = 64 * (blockIdx.x % 4) + threadIdx.x;
     const float *src = partial + ((size_t)row * 2 + g) * splits * 2048 + (h % 8) * 256 + d;
     float sum = 0.0f;
-    uint32_t s = 0;
-    for (; s + 8 <= splits; s += 8) {   // eight loads in flight, added in split order
-        float x[8];
+    for (uint32_t s = 0; s < splits; s += 32) {   // 32 loads in flight, added in split order
+        float x[32];
 #pragma unroll
-        for (int u = 0; u < 8; u++) x[u] = src[(size_t)(s + u) * 2048];
+        for (int u = 0; u < 32; u++) x[u] = src[(size_t)min(s + u, splits - 1) * 2048];
 #pragma unroll
-        for (int u = 0; u < 8; u++) sum += x[u];
+        for (int u = 0; u < 32; u++)
+            if (s + u < splits) sum += x[u];
     }
-    for (; s < splits; s++) sum += src[(size_t)s * 2048];
     const size_t i = ((size_t)row * 16 + h) * 256 + d;
     y[i] = sum * (1.0f / (1.0f + expf(-gate[i])));
 }
@@ -1107,6 +1112,7 @@ const char *launch_values_int8(Context &c, const View *b, int count, const boot_
     BOOT_REQUIRE(count >= 5, "batch_attention_values_int8 needs 5 bindings: scores, v, gate, y, vs");
     const uint64_t rows = p.m, K = p.k;
     if (rows == 0) return nullptr;
+    BOOT_REQUIRE(rows <= 65535, "batch_attention_values_int8 serves at most 65535 rows");   // the combine's grid
     const uint64_t length = (uint64_t)p.pos + rows;
     BOOT_REQUIRE(length <= K, "causal end pos+rows exceeds the score row stride K");
     BOOT_REQUIRE(b[0].bytes >= rows * 16 * K * 4, "scores buffer smaller than rows*16*K floats");
@@ -1123,7 +1129,6 @@ const char *launch_values_int8(Context &c, const View *b, int count, const boot_
     // 2 rows read V four times: 63.6 us); a row's result is the same in each
     const int per = rows >= 3 ? 4 : rows == 2 ? 2 : 1;
     const uint64_t zs = (rows + per - 1) / per;
-    BOOT_REQUIRE(zs <= 65535, "batch_attention_values_int8 serves at most 262140 rows");
     const dim3 vgrid((uint32_t)splits, 2, (uint32_t)zs);
     const float *sc = (const float *)b[0].ptr, *vsc = (const float *)b[4].ptr;
     const int8_t *vc = (const int8_t *)b[1].ptr;
@@ -1136,7 +1141,7 @@ const char *launch_values_int8(Context &c, const View *b, int count, const boot_
     else
         launch_timed(c, "values_partial_kernel", values_partial_kernel<1>, vgrid, dim3(256), sc, vc, vsc, part,
                      (uint32_t)rows, (uint32_t)K, p.pos, (uint32_t)splits);
-    launch_timed(c, "values_combine_kernel", values_combine_kernel, dim3(16, (uint32_t)rows), dim3(256),
+    launch_timed(c, "values_combine_kernel", values_combine_kernel, dim3(64, (uint32_t)rows), dim3(64),
                  (const float *)part, (const float *)b[2].ptr, (float *)b[3].ptr, (uint32_t)splits);
     return nullptr;
 }

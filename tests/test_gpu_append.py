@@ -235,7 +235,7 @@ def test_attention_dispatch_validation_errors(device):
     """The attention launchers reject, on the host and before any launch, what the
     reference's call sites never pass: a group size other than 8, K != Position + M,
     a history beyond the 262144-token window, missing or undersized or misaligned
-    bindings, and more than 64 decode rows."""
+    bindings, more than 64 decode rows, and more reader rows than the values merge's grid holds."""
     from bootstrap_hip import HipError
     rows, pos = 4, 100
     keys = pos + rows
@@ -254,6 +254,7 @@ def test_attention_dispatch_validation_errors(device):
         (name, KernelArgs(M=rows, K=keys, Position=pos, A=8), (q.at(4),) + bind[1:], "misaligned"),
         ("attention_decode_int8", KernelArgs(M=65, K=keys, Position=pos), bind, "at most 64 rows"),
         ("attention_decode_int8", KernelArgs(M=rows, K=keys, Position=pos), bind[:6], "needs 7 bindings"),
+        ("batch_attention_values_int8", KernelArgs(M=65536, K=65636, Position=pos), bind[:5], "at most 65535 rows"),
     ]
     for kernel, args, bindings, message in cases:
         device.begin()
