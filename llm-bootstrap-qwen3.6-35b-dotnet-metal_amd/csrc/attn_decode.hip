@@ -40,11 +40,16 @@ namespace {
 template <int kRows>
 __global__ __launch_bounds__(256) void scores_int8_kernel(const float *__restrict__ q, const int8_t *__restrict__ k,
                                                           float *__restrict__ scores, const float *__restrict__ ks,
-                                                          uint32_t rows, uint32_t K, uint32_t pos) {
+                                                          uint32_t rows, uint32_t K, uint32_t pos, uint32_t tiles,
+                                                          uint32_t zs) {
     typedef int v4i __attribute__((ext_vector_type(4)));
     __shared__ v4i qop[kRows][2][4][64];   // [row][set][64-dimension step][lane]
     __shared__ float qscale[kRows][8];
-    const uint32_t g = blockIdx.y, r0 = blockIdx.z * kRows;
+    // blocks are dealt to the XCDs round-robin by index: the row blocks of one (tile, group) pair
+    // are 8 apart, on one XCD at about the same time, so that the K tile they share comes from HBM once
+    const uint32_t xcd = blockIdx.x % 8, j = blockIdx.x / 8, pair = (j / zs) * 8 + xcd;
+    if (pair >= 2 * tiles) return;   // padding of the grid to whole rounds of 8
+    const uint32_t kt = pair / 2, g = pair % 2, r0 = (j % zs) * kRows;
     const uint32_t nr = min((uint32_t)kRows, rows - r0);
     const uint32_t length = min(pos + rows, K);   // the cache rows read (validated by the launcher)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n = lane & 15, qq = lane >> 4;
@@ -88,50 +93,60 @@ __global__ __launch_bounds__(256) void scores_int8_kernel(const float *__restric
     }
     __syncthreads();
     const bool lo_col = n >= 8;
+    // Two 16-token tiles at a time: after the hi/lo exchange lanes n < 8 finish the first and lanes
+    // n >= 8 the second, so that one store instruction writes 128 contiguous bytes of each head's row
+    // with every lane active.
 #pragma unroll 1
-    for (int tile = 0; tile < 4; tile++) {
-        const uint32_t tb = blockIdx.x * 256 + 64 * wave + 16 * tile;
-        if (tb >= K) break;   // wave-uniform
-        const uint32_t tk = min(tb + n, length - 1);   // the lane's K row (an existing one)
-        v4i kop[4];
+    for (int tp = 0; tp < 2; tp++) {
+        const uint32_t ta = kt * 256 + 64 * wave + 32 * tp;
+        if (ta >= K) break;   // wave-uniform
+        v4i kop[2][4];
+        float kss[2][4];
 #pragma unroll
-        for (int jj = 0; jj < 4; jj++)
-            kop[jj] = *reinterpret_cast<const v4i *>(k + ((size_t)tk * 2 + g) * 256 + 64 * jj + 16 * qq);
-        float kss[4];
+        for (int u = 0; u < 2; u++) {
+            const uint32_t tk = min(ta + 16 * u + n, length - 1);   // the lane's K row (an existing one)
 #pragma unroll
-        for (int i = 0; i < 4; i++) kss[i] = ks[(size_t)min(tb + 4 * qq + i, length - 1) * 2 + g];
+            for (int jj = 0; jj < 4; jj++)
+                kop[u][jj] = *reinterpret_cast<const v4i *>(k + ((size_t)tk * 2 + g) * 256 + 64 * jj + 16 * qq);
+#pragma unroll
+            for (int i = 0; i < 4; i++) kss[u][i] = ks[(size_t)min(ta + 16 * u + 4 * qq + i, length - 1) * 2 + g];
+        }
+        const uint32_t tb = ta + (lo_col ? 16 : 0);   // the tile this lane finishes
 #pragma unroll
         for (int r = 0; r < kRows; r++) {
             if ((uint32_t)r >= nr) break;   // uniform
-            v4i acc = {0, 0, 0, 0}, acc3 = {0, 0, 0, 0};
+            v4i acc[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}}, acc3[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
 #pragma unroll
-            for (int jj = 0; jj < 4; jj++) {
-                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop[jj], qop[r][0][jj][lane], acc, 0, 0, 0);
-                acc3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop[jj], qop[r][1][jj][lane], acc3, 0, 0, 0);
-            }
-            // token tb + 4qq + i, column n; the partner column n ^ 8 holds the other part of the head
+            for (int u = 0; u < 2; u++)
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) {
+                    acc[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop[u][jj], qop[r][0][jj][lane], acc[u], 0, 0, 0);
+                    acc3[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kop[u][jj], qop[r][1][jj][lane], acc3[u], 0, 0, 0);
+                }
+            // column n holds head n % 8's part q1 (n < 8) or q2 (n >= 8), both columns its q3; token
+            // tb + 4qq + i of this lane's tile
             const float qsc = qscale[r][n & 7];
             const uint32_t last = pos + r0 + r;   // the row's last visible key
             float *dst = scores + ((size_t)(r0 + r) * 16 + g * 8 + (n & 7)) * K;
             float out[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const int mine = acc[i], other = __shfl_xor(mine, 8, 64);
-                const float hi = (float)(lo_col ? other : mine), lo = (float)(lo_col ? mine : other);
-                const float full = fmaf((float)acc3[i], 1.0f / 64516.0f, fmaf(lo, 1.0f / 254.0f, hi)) * qsc;
+                const int ma = acc[0][i], oa = __shfl_xor(ma, 8, 64);
+                const int mb = acc[1][i], ob = __shfl_xor(mb, 8, 64);
+                const float hi = (float)(lo_col ? ob : ma), lo = (float)(lo_col ? mb : oa);
+                const int c3 = lo_col ? acc3[1][i] : acc3[0][i];
+                const float full = fmaf((float)c3, 1.0f / 64516.0f, fmaf(lo, 1.0f / 254.0f, hi)) * qsc;
                 const uint32_t t = tb + 4 * qq + i;
-                out[i] = t <= last ? full * kss[i] * (1.0f / 16.0f) : -INFINITY;
+                out[i] = t <= last ? full * (lo_col ? kss[1][i] : kss[0][i]) * (1.0f / 16.0f) : -INFINITY;
             }
             // the lane's four consecutive tokens as one 16-byte store where the row allows it
             const uint32_t t4 = tb + 4 * qq;
-            if (!lo_col) {
-                if (t4 + 3 < K && (reinterpret_cast<uintptr_t>(dst + t4) & 15) == 0) {
-                    *reinterpret_cast<float4 *>(dst + t4) = make_float4(out[0], out[1], out[2], out[3]);
-                } else {
+            if (t4 + 3 < K && (reinterpret_cast<uintptr_t>(dst + t4) & 15) == 0) {
+                *reinterpret_cast<float4 *>(dst + t4) = make_float4(out[0], out[1], out[2], out[3]);
+            } else {
 #pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        if (t4 + i < K) dst[t4 + i] = out[i];
-                }
+                for (int i = 0; i < 4; i++)
+                    if (t4 + i < K) dst[t4 + i] = out[i];
             }
         }
     }
@@ -235,12 +250,15 @@ template <int kRows>
 __global__ __launch_bounds__(256) void values_partial_kernel(const float *__restrict__ scores,
                                                              const int8_t *__restrict__ v, const float *__restrict__ vs,
                                                              float *__restrict__ partial, uint32_t rows, uint32_t K,
-                                                             uint32_t pos, uint32_t splits) {
+                                                             uint32_t pos, uint32_t splits, uint32_t zs) {
     typedef _Float16 half4 __attribute__((ext_vector_type(4)));
     constexpr int kEnt = 2 * kRows;                    // staging (row, head) pairs per thread, one token each
     __shared__ uint2 bs[kRows][4][64];                  // B operands [row][k-step][lane]
     __shared__ float vred[4][kRows];
-    const uint32_t split = blockIdx.x, g = blockIdx.y, r0 = blockIdx.z * kRows;
+    // the row blocks of one (split, group) pair 8 blocks apart: one XCD reads the pair's V once
+    const uint32_t xcd = blockIdx.x % 8, jb = blockIdx.x / 8, pair = (jb / zs) * 8 + xcd;
+    if (pair >= 2 * splits) return;   // padding of the grid to whole rounds of 8
+    const uint32_t split = pair / 2, g = pair % 2, r0 = (jb % zs) * kRows;
     const uint32_t nr = min((uint32_t)kRows, rows - r0);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n = lane & 15, qq = lane >> 4;
     const uint32_t t0 = split * kValuesSplit;
@@ -1069,19 +1087,20 @@ const char *launch_scores_int8(Context &c, const View *b, int count, const boot_
     const int per = rows >= 3 ? 4 : rows == 2 ? 2 : 1;
     const uint64_t zs = (rows + per - 1) / per;
     BOOT_REQUIRE(zs <= 65535, "batch_attention_scores_int8 serves at most 262140 rows");
-    const dim3 sgrid((uint32_t)((K + 255) / 256), 2, (uint32_t)zs);
+    const uint64_t ktiles = (K + 255) / 256;
+    const dim3 sgrid((uint32_t)((2 * ktiles + 7) / 8 * 8 * zs));
     const float *qp = (const float *)b[0].ptr, *ksp = (const float *)b[3].ptr;
     const int8_t *kp = (const int8_t *)b[1].ptr;
     float *sp = (float *)b[2].ptr;
     if (per == 4)
         launch_timed(c, "scores_int8_kernel", scores_int8_kernel<4>, sgrid, dim3(256), qp, kp, sp, ksp, (uint32_t)rows,
-                     (uint32_t)K, p.pos);
+                     (uint32_t)K, p.pos, (uint32_t)ktiles, (uint32_t)zs);
     else if (per == 2)
         launch_timed(c, "scores_int8_kernel", scores_int8_kernel<2>, sgrid, dim3(256), qp, kp, sp, ksp, (uint32_t)rows,
-                     (uint32_t)K, p.pos);
+                     (uint32_t)K, p.pos, (uint32_t)ktiles, (uint32_t)zs);
     else
         launch_timed(c, "scores_int8_kernel", scores_int8_kernel<1>, sgrid, dim3(256), qp, kp, sp, ksp, (uint32_t)rows,
-                     (uint32_t)K, p.pos);
+                     (uint32_t)K, p.pos, (uint32_t)ktiles, (uint32_t)zs);
     return nullptr;
 }
 
@@ -1129,18 +1148,18 @@ const char *launch_values_int8(Context &c, const View *b, int count, const boot_
     // 2 rows read V four times: 63.6 us); a row's result is the same in each
     const int per = rows >= 3 ? 4 : rows == 2 ? 2 : 1;
     const uint64_t zs = (rows + per - 1) / per;
-    const dim3 vgrid((uint32_t)splits, 2, (uint32_t)zs);
+    const dim3 vgrid((uint32_t)((2 * splits + 7) / 8 * 8 * zs));
     const float *sc = (const float *)b[0].ptr, *vsc = (const float *)b[4].ptr;
     const int8_t *vc = (const int8_t *)b[1].ptr;
     if (per == 4)
         launch_timed(c, "values_partial_kernel", values_partial_kernel<4>, vgrid, dim3(256), sc, vc, vsc, part,
-                     (uint32_t)rows, (uint32_t)K, p.pos, (uint32_t)splits);
+                     (uint32_t)rows, (uint32_t)K, p.pos, (uint32_t)splits, (uint32_t)zs);
     else if (per == 2)
         launch_timed(c, "values_partial_kernel", values_partial_kernel<2>, vgrid, dim3(256), sc, vc, vsc, part,
-                     (uint32_t)rows, (uint32_t)K, p.pos, (uint32_t)splits);
+                     (uint32_t)rows, (uint32_t)K, p.pos, (uint32_t)splits, (uint32_t)zs);
     else
         launch_timed(c, "values_partial_kernel", values_partial_kernel<1>, vgrid, dim3(256), sc, vc, vsc, part,
-                     (uint32_t)rows, (uint32_t)K, p.pos, (uint32_t)splits);
+                     (uint32_t)rows, (uint32_t)K, p.pos, (uint32_t)splits, (uint32_t)zs);
     launch_timed(c, "values_combine_kernel", values_combine_kernel, dim3(64, (uint32_t)rows), dim3(64),
                  (const float *)part, (const float *)b[2].ptr, (float *)b[3].ptr, (uint32_t)splits);
     return nullptr;
