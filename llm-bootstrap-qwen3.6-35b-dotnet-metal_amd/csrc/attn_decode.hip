@@ -36,7 +36,8 @@ namespace {
 // combination is FP32 per element: a row's scores do not depend on the rows it is dispatched
 // with. Work-group (256 tokens, KV group, kRows rows): the query operands of its rows in LDS
 // (16 columns: 8 heads x {q1, q2}, and 8 heads x q3 twice), wave w takes tokens 64w .. 64w + 63
-// in 16-token tiles; each K operand (16 bytes of a token's row per lane) feeds 2 kRows MFMAs.
+// in pairs of 16-token tiles; each K operand (16 bytes of a token's row per lane) feeds 2 kRows
+// MFMAs.
 template <int kRows>
 __global__ __launch_bounds__(256) void scores_int8_kernel(const float *__restrict__ q, const int8_t *__restrict__ k,
                                                           float *__restrict__ scores, const float *__restrict__ ks,
