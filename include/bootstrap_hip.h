@@ -62,7 +62,10 @@ int boot_clear(void *ctx, void *buf);
  * Launch geometry is chosen by the library from the arguments; x..tz are the
  * caller's Metal thread counts and are only validated for consistency where
  * a kernel needs them. `indirect` must be NULL (no INT8 kernel is indirect).
- * Sizes are validated against the bound buffers before launch. */
+ * Sizes are validated against the bound buffers before launch. A dispatch with
+ * no rows (M = 0; attention_softmax: no 256-thread row groups) launches nothing
+ * and succeeds, as a zero-thread Metal dispatch does, except the single-row
+ * attention_decode_append_int8, which requires M = 1. */
 int boot_dispatch(void *ctx, const char *name, void **buffers, const uint64_t *offsets, int count,
                   const void *params, int param_bytes, uint32_t x, uint32_t y, uint32_t z,
                   uint32_t tx, uint32_t ty, uint32_t tz, void *indirect, uint64_t indirect_offset);
