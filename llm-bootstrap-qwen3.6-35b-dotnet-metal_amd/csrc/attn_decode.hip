@@ -239,23 +239,26 @@ constexpr int kValuesSplit = 512;
 // the 16 columns 8 heads x {FP16 hi, FP16 lo} (vs_r the row's largest V scale over its tokens of
 // the split, so that B <= 2^15; hi + lo keeps about 22 bits), the result times vs_r / 2^15. The
 // factor 2^15 keeps the probabilities of a long, flat row (p ~ 1 / K) out of FP16's subnormals
-// (below 2^-14), where hi and lo would keep only a few bits. Wave w takes
-// dimensions 64w .. 64w + 63; a 64-token block is four k-steps, lane (n, qq) of step s holding
-// tokens 16qq + 4s .. + 3 of the block for both operands (one 16-byte code load per dimension
-// tile covers its four steps), and the next block's loads are issued before the current block is
-// staged. Every quantity of a row depends on that row's range only, whatever kRows is.
+// (below 2^-14), where hi and lo would keep only a few bits. Eight waves, wave w taking
+// dimensions 32w .. 32w + 31 (96 registers: two work-groups per CU; four waves with 64 dimensions
+// each held 168, three per CU, 21.5 against 18.9 us at 4 rows over 30000 keys); a 64-token block
+// is four k-steps, lane (n, qq) of step s holding tokens 16qq + 4s .. + 3 of the block for both
+// operands (one 16-byte code load per dimension tile covers its four steps), and the next block's
+// loads are issued before the current block is staged. Every quantity of a row depends on that
+// row's range only, whatever kRows is.
 constexpr int kVmBlock = 64;
 constexpr float kValuesScale = 32768.0f;   // 2^15: B's factor
 
 template <int kRows>
-__global__ __launch_bounds__(256) void values_partial_kernel(const float *__restrict__ scores,
+__global__ __launch_bounds__(512) void values_partial_kernel(const float *__restrict__ scores,
                                                              const int8_t *__restrict__ v, const float *__restrict__ vs,
                                                              float *__restrict__ partial, uint32_t rows, uint32_t K,
                                                              uint32_t pos, uint32_t splits, uint32_t zs) {
     typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-    constexpr int kEnt = 2 * kRows;                    // staging (row, head) pairs per thread, one token each
+    constexpr int kWaves = 8;                           // wave w: dimensions 32w .. 32w + 31
+    constexpr int kEnt = kRows;                         // staging (row, head) pairs per thread, one token each
     __shared__ uint2 bs[kRows][4][64];                  // B operands [row][k-step][lane]
-    __shared__ float vred[4][kRows];
+    __shared__ float vred[kWaves][kRows];
     // the row blocks of one (split, group) pair 8 blocks apart: one XCD reads the pair's V once
     const uint32_t xcd = blockIdx.x % 8, jb = blockIdx.x / 8, pair = (jb / zs) * 8 + xcd;
     if (pair >= 2 * splits) return;   // padding of the grid to whole rounds of 8
@@ -272,8 +275,8 @@ __global__ __launch_bounds__(256) void values_partial_kernel(const float *__rest
         for (int r = 0; r < kRows; r++) vm[r] = 0.0f;
         if (t0 < t1)
 #pragma unroll
-            for (int k = 0; k < kValuesSplit / 256; k++) {
-                const uint32_t t = t0 + tid + 256 * k;
+            for (int k = 0; k < kValuesSplit / 512; k++) {
+                const uint32_t t = t0 + tid + 512 * k;
                 const float x = vs[(size_t)min(t, t1 - 1) * 2 + g];
 #pragma unroll
                 for (int r = 0; r < kRows; r++)
@@ -287,32 +290,36 @@ __global__ __launch_bounds__(256) void values_partial_kernel(const float *__rest
         }
         __syncthreads();
 #pragma unroll
-        for (int r = 0; r < kRows; r++) vr[r] = fmaxf(fmaxf(vred[0][r], vred[1][r]), fmaxf(vred[2][r], vred[3][r]));
-    }
-    floatx4 acc[4][kRows];
+        for (int r = 0; r < kRows; r++) {
+            vr[r] = vred[0][r];
 #pragma unroll
-    for (int dt = 0; dt < 4; dt++)
+            for (int w = 1; w < kWaves; w++) vr[r] = fmaxf(vr[r], vred[w][r]);
+        }
+    }
+    floatx4 acc[2][kRows];
+#pragma unroll
+    for (int dt = 0; dt < 2; dt++)
 #pragma unroll
         for (int r = 0; r < kRows; r++) acc[dt][r] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    // staging: thread T takes token T % 64 of the block for the (row, head) pairs T / 64 + 4i, so that
+    // staging: thread T takes token T % 64 of the block for the (row, head) pairs T / 64 + 8i, so that
     // a wave's score loads read 64 consecutive tokens of one pair
     const int tok = tid & 63, pair0 = tid >> 6;
     struct Loads {
         float sc[kEnt], sv;
-        uint4 w4[4];   // the wave's four dimension tiles: dimension 64 wave + 16 dt + n, tokens 16 qq .. + 15
+        uint4 w4[2];   // the wave's two dimension tiles: dimension 32 wave + 16 dt + n, tokens 16 qq .. + 15
     };
     auto load = [&](Loads &L, uint32_t tb) __attribute__((always_inline)) {
         const uint32_t t = tb + tok;
         L.sv = vs[(size_t)min(t, t1 - 1) * 2 + g];
 #pragma unroll
         for (int i = 0; i < kEnt; i++) {
-            const int rh = pair0 + 4 * i, r = rh >> 3, h = rh & 7;
+            const int rh = pair0 + 8 * i, r = rh >> 3, h = rh & 7;
             const bool live = (uint32_t)r < nr && t < pos + r0 + r + 1;
             L.sc[i] = live ? scores[((size_t)(r0 + r) * 16 + g * 8 + h) * K + t] : 0.0f;
         }
 #pragma unroll
-        for (int dt = 0; dt < 4; dt++)
-            L.w4[dt] = *reinterpret_cast<const uint4 *>(v + value_index((uint64_t)tb * 2 + g, 64 * wave + 16 * dt + n) + 16 * qq);
+        for (int dt = 0; dt < 2; dt++)
+            L.w4[dt] = *reinterpret_cast<const uint4 *>(v + value_index((uint64_t)tb * 2 + g, 32 * wave + 16 * dt + n) + 16 * qq);
     };
     Loads cur, nxt;
     if (t0 < t1) load(cur, t0);
@@ -326,7 +333,7 @@ __global__ __launch_bounds__(256) void values_partial_kernel(const float *__rest
             const int s = (tok & 15) >> 2, j = tok & 3, lrow = 16 * (tok >> 4);
 #pragma unroll
             for (int i = 0; i < kEnt; i++) {
-                const int rh = pair0 + 4 * i, r = rh >> 3, h = rh & 7;
+                const int rh = pair0 + 8 * i, r = rh >> 3, h = rh & 7;
                 if ((uint32_t)r < nr) {
                     const float inv = vr[r] > 0.0f ? kValuesScale / vr[r] : 0.0f;
                     const float x = cur.sc[i] * cur.sv * inv;
@@ -339,9 +346,9 @@ __global__ __launch_bounds__(256) void values_partial_kernel(const float *__rest
         __syncthreads();
 #pragma unroll
         for (int s = 0; s < 4; s++) {
-            half4 a[4];
+            half4 a[2];
 #pragma unroll
-            for (int dt = 0; dt < 4; dt++) {
+            for (int dt = 0; dt < 2; dt++) {
                 const uint4 &w = cur.w4[dt];
                 const uint32_t word = s == 0 ? w.x : s == 1 ? w.y : s == 2 ? w.z : w.w;
                 uint32_t h0, h1;
@@ -353,25 +360,25 @@ __global__ __launch_bounds__(256) void values_partial_kernel(const float *__rest
                 if ((uint32_t)r >= nr) break;   // uniform
                 const half4 b = __builtin_bit_cast(half4, bs[r][s][lane]);
 #pragma unroll
-                for (int dt = 0; dt < 4; dt++) acc[dt][r] = __builtin_amdgcn_mfma_f32_16x16x16f16(a[dt], b, acc[dt][r], 0, 0, 0);
+                for (int dt = 0; dt < 2; dt++) acc[dt][r] = __builtin_amdgcn_mfma_f32_16x16x16f16(a[dt], b, acc[dt][r], 0, 0, 0);
             }
         }
         if (more) cur = nxt;
     }
-    // the lo column n + 8 joins the hi column n (head n); lanes n < 8 write dimensions 64 wave + 16 dt + 4 qq + e
+    // the lo column n + 8 joins the hi column n (head n); lanes n < 8 write dimensions 32 wave + 16 dt + 4 qq + e
 #pragma unroll
     for (int r = 0; r < kRows; r++) {
         if ((uint32_t)r >= nr) break;
         float *out = partial + (((size_t)(r0 + r) * 2 + g) * splits + split) * 2048;
         const float f = vr[r] * (1.0f / kValuesScale);   // exact: a power of two
 #pragma unroll
-        for (int dt = 0; dt < 4; dt++) {
+        for (int dt = 0; dt < 2; dt++) {
             float4 o4;
             o4.x = (acc[dt][r][0] + __shfl_xor(acc[dt][r][0], 8, 64)) * f;
             o4.y = (acc[dt][r][1] + __shfl_xor(acc[dt][r][1], 8, 64)) * f;
             o4.z = (acc[dt][r][2] + __shfl_xor(acc[dt][r][2], 8, 64)) * f;
             o4.w = (acc[dt][r][3] + __shfl_xor(acc[dt][r][3], 8, 64)) * f;
-            if (n < 8) *reinterpret_cast<float4 *>(out + n * 256 + 64 * wave + 16 * dt + 4 * qq) = o4;
+            if (n < 8) *reinterpret_cast<float4 *>(out + n * 256 + 32 * wave + 16 * dt + 4 * qq) = o4;
         }
     }
 }
@@ -1153,13 +1160,13 @@ const char *launch_values_int8(Context &c, const View *b, int count, const boot_
     const float *sc = (const float *)b[0].ptr, *vsc = (const float *)b[4].ptr;
     const int8_t *vc = (const int8_t *)b[1].ptr;
     if (per == 4)
-        launch_timed(c, "values_partial_kernel", values_partial_kernel<4>, vgrid, dim3(256), sc, vc, vsc, part,
+        launch_timed(c, "values_partial_kernel", values_partial_kernel<4>, vgrid, dim3(512), sc, vc, vsc, part,
                      (uint32_t)rows, (uint32_t)K, p.pos, (uint32_t)splits, (uint32_t)zs);
     else if (per == 2)
-        launch_timed(c, "values_partial_kernel", values_partial_kernel<2>, vgrid, dim3(256), sc, vc, vsc, part,
+        launch_timed(c, "values_partial_kernel", values_partial_kernel<2>, vgrid, dim3(512), sc, vc, vsc, part,
                      (uint32_t)rows, (uint32_t)K, p.pos, (uint32_t)splits, (uint32_t)zs);
     else
-        launch_timed(c, "values_partial_kernel", values_partial_kernel<1>, vgrid, dim3(256), sc, vc, vsc, part,
+        launch_timed(c, "values_partial_kernel", values_partial_kernel<1>, vgrid, dim3(512), sc, vc, vsc, part,
                      (uint32_t)rows, (uint32_t)K, p.pos, (uint32_t)splits, (uint32_t)zs);
     launch_timed(c, "values_combine_kernel", values_combine_kernel, dim3(64, (uint32_t)rows), dim3(64),
                  (const float *)part, (const float *)b[2].ptr, (float *)b[3].ptr, (uint32_t)splits);
