@@ -34,15 +34,15 @@ namespace {
 // into three INT8 parts, q ~= s_q (q1 + q2 / 254 + q3 / 254^2) with s_q = max|q| / 127 (error
 // <= 6.1e-8 max|q| per element), the dot products with the codes are exact integers, and their
 // combination is FP32 per element: a row's scores do not depend on the rows it is dispatched
-// with. Work-group (256 tokens, KV group, kRows rows): the query operands of its rows in LDS
-// (16 columns: 8 heads x {q1, q2}, and 8 heads x q3 twice), wave w takes tokens 64w .. 64w + 63
-// in pairs of 16-token tiles; each K operand (16 bytes of a token's row per lane) feeds 2 kRows
+// with. Work-group (span = 256 or 512 tokens, KV group, kRows rows): the query operands of its rows
+// in LDS (16 columns: 8 heads x {q1, q2}, and 8 heads x q3 twice), wave w takes the span's quarter
+// w in pairs of 16-token tiles; each K operand (16 bytes of a token's row per lane) feeds 2 kRows
 // MFMAs.
 template <int kRows>
 __global__ __launch_bounds__(256) void scores_int8_kernel(const float *__restrict__ q, const int8_t *__restrict__ k,
                                                           float *__restrict__ scores, const float *__restrict__ ks,
                                                           uint32_t rows, uint32_t K, uint32_t pos, uint32_t tiles,
-                                                          uint32_t zs) {
+                                                          uint32_t zs, uint32_t span) {
     typedef int v4i __attribute__((ext_vector_type(4)));
     __shared__ v4i qop[kRows][2][4][64];   // [row][set][64-dimension step][lane]
     __shared__ float qscale[kRows][8];
@@ -96,10 +96,11 @@ __global__ __launch_bounds__(256) void scores_int8_kernel(const float *__restric
     const bool lo_col = n >= 8;
     // Two 16-token tiles at a time: after the hi/lo exchange lanes n < 8 finish the first and lanes
     // n >= 8 the second, so that one store instruction writes 128 contiguous bytes of each head's row
-    // with every lane active.
+    // with every lane active. The work-group's `span` tokens (256 or 512) are split over the waves.
+    const uint32_t per_wave = span / 4;
 #pragma unroll 1
-    for (int tp = 0; tp < 2; tp++) {
-        const uint32_t ta = kt * 256 + 64 * wave + 32 * tp;
+    for (uint32_t tp = 0; tp < per_wave / 32; tp++) {
+        const uint32_t ta = kt * span + per_wave * wave + 32 * tp;
         if (ta >= K) break;   // wave-uniform
         v4i kop[2][4];
         float kss[2][4];
@@ -1095,20 +1096,26 @@ const char *launch_scores_int8(Context &c, const View *b, int count, const boot_
     const int per = rows >= 3 ? 4 : rows == 2 ? 2 : 1;
     const uint64_t zs = (rows + per - 1) / per;
     BOOT_REQUIRE(zs <= 65535, "batch_attention_scores_int8 serves at most 262140 rows");
-    const uint64_t ktiles = (K + 255) / 256;
+    // tokens per work-group: 512 where the grid still holds four work-groups per CU (each one then
+    // builds its rows' query operands for twice the tokens: 8 rows over 131072 keys 38.3 -> 32.7
+    // us), else 256 (4 rows over 30000 keys: 12.5 us, against 18.1 with 512); a score does not
+    // depend on the span
+    const uint64_t wide = (K + 511) / 512;
+    const uint32_t span = 2 * wide * zs >= 4 * (uint64_t)std::max(1, context_cus(c)) ? 512u : 256u;
+    const uint64_t ktiles = (K + span - 1) / span;
     const dim3 sgrid((uint32_t)((2 * ktiles + 7) / 8 * 8 * zs));
     const float *qp = (const float *)b[0].ptr, *ksp = (const float *)b[3].ptr;
     const int8_t *kp = (const int8_t *)b[1].ptr;
     float *sp = (float *)b[2].ptr;
     if (per == 4)
         launch_timed(c, "scores_int8_kernel", scores_int8_kernel<4>, sgrid, dim3(256), qp, kp, sp, ksp, (uint32_t)rows,
-                     (uint32_t)K, p.pos, (uint32_t)ktiles, (uint32_t)zs);
+                     (uint32_t)K, p.pos, (uint32_t)ktiles, (uint32_t)zs, span);
     else if (per == 2)
         launch_timed(c, "scores_int8_kernel", scores_int8_kernel<2>, sgrid, dim3(256), qp, kp, sp, ksp, (uint32_t)rows,
-                     (uint32_t)K, p.pos, (uint32_t)ktiles, (uint32_t)zs);
+                     (uint32_t)K, p.pos, (uint32_t)ktiles, (uint32_t)zs, span);
     else
         launch_timed(c, "scores_int8_kernel", scores_int8_kernel<1>, sgrid, dim3(256), qp, kp, sp, ksp, (uint32_t)rows,
-                     (uint32_t)K, p.pos, (uint32_t)ktiles, (uint32_t)zs);
+                     (uint32_t)K, p.pos, (uint32_t)ktiles, (uint32_t)zs, span);
     return nullptr;
 }
 
