@@ -135,7 +135,6 @@ __device__ __forceinline__ void o_mfma(floatx16 &o, const half8 &a, const half8 
 // unchanged, so their consumers cannot be scheduled ahead of it (the scheduler places an assembly
 // statement's independent neighbours freely).
 __device__ __forceinline__ void after_mfma(float &z, float &w) { asm volatile("" : "+v"(z), "+v"(w)); }
-__device__ __forceinline__ void after_mfma(uint32_t &x, uint32_t &y) { asm volatile("" : "+v"(x), "+v"(y)); }
 __device__ __forceinline__ void after_mfma(uint32_t &x, uint32_t &y, uint32_t &z, uint32_t &w) {
     asm volatile("" : "+v"(x), "+v"(y), "+v"(z), "+v"(w));
 }
@@ -144,7 +143,6 @@ __device__ __forceinline__ void after_mfma(uint32_t &x, uint32_t &y, uint32_t &z
 // collecting in long runs the matrix pipe waits through.
 __device__ __forceinline__ void before_mfma(float x, float y) { asm volatile("" ::"v"(x), "v"(y)); }
 __device__ __forceinline__ void before_mfma(float x, float y, uint32_t z) { asm volatile("" ::"v"(x), "v"(y), "v"(z)); }
-__device__ __forceinline__ void before_mfma(uint32_t x, uint32_t y) { asm volatile("" ::"v"(x), "v"(y)); }
 
 // ---------------------------------------------------------------- prefill, one wave per SIMD
 //
