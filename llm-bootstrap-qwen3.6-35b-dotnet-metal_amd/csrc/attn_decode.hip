@@ -258,7 +258,13 @@ __global__ __launch_bounds__(512) void values_partial_kernel(const float *__rest
     typedef _Float16 half4 __attribute__((ext_vector_type(4)));
     constexpr int kWaves = 8;                           // wave w: dimensions 32w .. 32w + 31
     constexpr int kEnt = kRows;                         // staging (row, head) pairs per thread, one token each
-    __shared__ uint2 bs[kRows][4][64];                  // B operands [row][k-step][lane]
+    // B operands [row][k-step][slot]: lane L's operand in slot L ^ ((L / 16) % 4 * 2), each k-step row
+    // padded by one slot. A staging store writes one (row, head)'s 64 tokens, which fall in 16
+    // slots (4 k-steps x 4 token blocks); without the padding and the XOR the four k-steps (512 bytes
+    // apart) and token blocks 0 and 2 share their banks, 8 to 16 lanes per bank; with them the 16
+    // slots cover 32 banks. The operand reads (64 slots of one k-step row) stay conflict-free.
+    __shared__ uint2 bs[kRows][4][65];
+    auto bslot = [](int L) __attribute__((always_inline)) { return L ^ ((L >> 3) & 6); };
     __shared__ float vred[kWaves][kRows];
     // the row blocks of one (split, group) pair 8 blocks apart: one XCD reads the pair's V once
     const uint32_t xcd = blockIdx.x % 8, jb = blockIdx.x / 8, pair = (jb / zs) * 8 + xcd;
@@ -339,8 +345,8 @@ __global__ __launch_bounds__(512) void values_partial_kernel(const float *__rest
                     const float inv = vr[r] > 0.0f ? kValuesScale / vr[r] : 0.0f;
                     const float x = cur.sc[i] * cur.sv * inv;
                     const _Float16 hi = (_Float16)x, lo = (_Float16)(x - (float)hi);
-                    reinterpret_cast<_Float16 *>(&bs[r][s][lrow + h])[j] = hi;
-                    reinterpret_cast<_Float16 *>(&bs[r][s][lrow + h + 8])[j] = lo;
+                    reinterpret_cast<_Float16 *>(&bs[r][s][bslot(lrow + h)])[j] = hi;
+                    reinterpret_cast<_Float16 *>(&bs[r][s][bslot(lrow + h + 8)])[j] = lo;
                 }
             }
         }
@@ -359,7 +365,7 @@ __global__ __launch_bounds__(512) void values_partial_kernel(const float *__rest
 #pragma unroll
             for (int r = 0; r < kRows; r++) {
                 if ((uint32_t)r >= nr) break;   // uniform
-                const half4 b = __builtin_bit_cast(half4, bs[r][s][lane]);
+                const half4 b = __builtin_bit_cast(half4, bs[r][s][bslot(lane)]);
 #pragma unroll
                 for (int dt = 0; dt < 2; dt++) acc[dt][r] = __builtin_amdgcn_mfma_f32_16x16x16f16(a[dt], b, acc[dt][r], 0, 0, 0);
             }
