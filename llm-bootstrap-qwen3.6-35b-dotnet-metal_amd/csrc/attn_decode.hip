@@ -257,7 +257,6 @@ __global__ __launch_bounds__(512) void values_partial_kernel(const float *__rest
                                                              uint32_t pos, uint32_t splits, uint32_t zs) {
     typedef _Float16 half4 __attribute__((ext_vector_type(4)));
     constexpr int kWaves = 8;                           // wave w: dimensions 32w .. 32w + 31
-    constexpr int kEnt = kRows;                         // staging (row, head) pairs per thread, one token each
     // B operands [row][k-step][slot]: lane L's operand in slot L ^ ((L / 16) % 4 * 2), each k-step row
     // padded by one slot. A staging store writes one (row, head)'s 64 tokens, which fall in 16
     // slots (4 k-steps x 4 token blocks); without the padding and the XOR the four k-steps (512 bytes
@@ -308,21 +307,23 @@ __global__ __launch_bounds__(512) void values_partial_kernel(const float *__rest
     for (int dt = 0; dt < 2; dt++)
 #pragma unroll
         for (int r = 0; r < kRows; r++) acc[dt][r] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-    // staging: thread T takes token T % 64 of the block for the (row, head) pairs T / 64 + 8i, so that
-    // a wave's score loads read 64 consecutive tokens of one pair
-    const int tok = tid & 63, pair0 = tid >> 6;
+    // staging: thread T takes token T % 64 of the block for row i, head T / 64 (the wave: uniform) of
+    // every row i, so that a wave's score loads read 64 consecutive tokens of one (row, head). The
+    // loads are unconditional (row and token clamped into the rows and keys that exist) and the
+    // causal mask a select at staging time (a select at the load would wait for it there), so no
+    // load sits under a per-lane branch.
+    const int tok = tid & 63, sh = __builtin_amdgcn_readfirstlane(tid >> 6);
     struct Loads {
-        float sc[kEnt], sv;
+        float sc[kRows], sv;
         uint4 w4[2];   // the wave's two dimension tiles: dimension 32 wave + 16 dt + n, tokens 16 qq .. + 15
     };
     auto load = [&](Loads &L, uint32_t tb) __attribute__((always_inline)) {
-        const uint32_t t = tb + tok;
-        L.sv = vs[(size_t)min(t, t1 - 1) * 2 + g];
+        const uint32_t t = tb + tok, tc = min(t, t1 - 1);
+        L.sv = vs[(size_t)tc * 2 + g];
 #pragma unroll
-        for (int i = 0; i < kEnt; i++) {
-            const int rh = pair0 + 8 * i, r = rh >> 3, h = rh & 7;
-            const bool live = (uint32_t)r < nr && t < pos + r0 + r + 1;
-            L.sc[i] = live ? scores[((size_t)(r0 + r) * 16 + g * 8 + h) * K + t] : 0.0f;
+        for (int i = 0; i < kRows; i++) {
+            const uint32_t rc = min((uint32_t)i, nr - 1);
+            L.sc[i] = scores[((size_t)(r0 + rc) * 16 + g * 8 + sh) * K + tc];
         }
 #pragma unroll
         for (int dt = 0; dt < 2; dt++)
@@ -339,14 +340,14 @@ __global__ __launch_bounds__(512) void values_partial_kernel(const float *__rest
             // of lane 16 (tok / 16) + column
             const int s = (tok & 15) >> 2, j = tok & 3, lrow = 16 * (tok >> 4);
 #pragma unroll
-            for (int i = 0; i < kEnt; i++) {
-                const int rh = pair0 + 8 * i, r = rh >> 3, h = rh & 7;
-                if ((uint32_t)r < nr) {
-                    const float inv = vr[r] > 0.0f ? kValuesScale / vr[r] : 0.0f;
-                    const float x = cur.sc[i] * cur.sv * inv;
+            for (int i = 0; i < kRows; i++) {
+                if ((uint32_t)i < nr) {   // uniform
+                    const float inv = vr[i] > 0.0f ? kValuesScale / vr[i] : 0.0f;
+                    const float p = tb + tok < pos + r0 + i + 1 ? cur.sc[i] : 0.0f;   // the causal mask
+                    const float x = p * cur.sv * inv;
                     const _Float16 hi = (_Float16)x, lo = (_Float16)(x - (float)hi);
-                    reinterpret_cast<_Float16 *>(&bs[r][s][bslot(lrow + h)])[j] = hi;
-                    reinterpret_cast<_Float16 *>(&bs[r][s][bslot(lrow + h + 8)])[j] = lo;
+                    reinterpret_cast<_Float16 *>(&bs[i][s][bslot(lrow + sh)])[j] = hi;
+                    reinterpret_cast<_Float16 *>(&bs[i][s][bslot(lrow + sh + 8)])[j] = lo;
                 }
             }
         }
