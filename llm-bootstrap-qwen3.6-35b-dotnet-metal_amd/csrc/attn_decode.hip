@@ -613,7 +613,7 @@ __device__ __attribute__((always_inline)) inline void patch_v(VRegs &r, int tid,
 // {q1, q2}, and a second product for q3), and turns them into probabilities in base 2 against a running reference
 // shared by the work-group; the waves exchange those P operands through LDS and wave w
 // accumulates O^T[d][n] += V^T[d][t] . Px[t][n] for dimensions 32w..32w+31 over all 128
-// tokens (16x16x16 FP16 MFMA), so no wave merge of O remains at the end. Px = p * vs /
+// tokens (16x16x32 FP16 MFMA), so no wave merge of O remains at the end. Px = p * vs /
 // vs_ref split into FP16 hi + lo; vs_ref, the split's largest V scale, keeps Px below
 // 256 and multiplies the result once. Lane l holds MFMA column n = l % 16 and
 // token/k group qq = l / 16.
@@ -883,19 +883,27 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
             }
             l += total_prev;   // this wave's tokens
             // O^T[d][n] += V^T[d][t] P[t][n] for this wave's 32 dimensions over the chunk's 128
-            // tokens: k-step src takes wave src's tokens 16 src..16 src+15 and P operand
+            // tokens on v_mfma_f32_16x16x32_f16: k-step s takes waves 2s and 2s + 1's tokens (32),
+            // lane (n, qq) tokens 8 (qq % 2) .. + 7 of wave 2s + qq / 2, i.e. the published P
+            // operands of lanes n + 32 (qq % 2) and n + 32 (qq % 2) + 16 of that wave and 8 codes
+            // (one 8-byte read) of its V piece. Against 16 MFMAs of 16 tokens with a 4-byte read
+            // each: half the MFMAs, dependent steps and V reads (29.6-30.0 against 30.2-30.3 us
+            // per layer step at 131073)
             const ChunkLds &b = bufs[slot];
 #pragma unroll
-            for (int src = 0; src < kDecodeWaves; src++) {
-                const half4 ps = __builtin_bit_cast(half4, pshare[slot][src][lane]);
+            for (int s = 0; s < kDecodeWaves / 2; s++) {
+                const int src = 2 * s + (qq >> 1);
+                const uint2 pa = pshare[slot][src][n + 32 * (qq & 1)], pb = pshare[slot][src][n + 32 * (qq & 1) + 16];
+                const half8 ps = __builtin_bit_cast(half8, make_uint4(pa.x, pa.y, pb.x, pb.y));
 #pragma unroll
                 for (int jj = 0; jj < 2; jj++) {
                     const int d = 16 * (2 * wave + jj) + n;
-                    const uint32_t w4 = reinterpret_cast<const uint32_t *>(&b.v[d][src ^ ((d >> 1) & 7)])[qq];
-                    uint32_t h0, h1;
-                    i8x4_to_f16(w4, h0, h1);
-                    const half4 va4 = __builtin_bit_cast(half4, make_uint2(h0, h1));
-                    o[jj] = __builtin_amdgcn_mfma_f32_16x16x16f16(va4, ps, o[jj], 0, 0, 0);
+                    const uint2 w8 = reinterpret_cast<const uint2 *>(&b.v[d][src ^ ((d >> 1) & 7)])[qq & 1];
+                    uint32_t h0, h1, h2, h3;
+                    i8x4_to_f16(w8.x, h0, h1);
+                    i8x4_to_f16(w8.y, h2, h3);
+                    const half8 va8 = __builtin_bit_cast(half8, make_uint4(h0, h1, h2, h3));
+                    o[jj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va8, ps, o[jj], 0, 0, 0);
                 }
             }
         }
