@@ -900,8 +900,7 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
                     const int d = 16 * (2 * wave + jj) + n;
                     const uint2 w8 = reinterpret_cast<const uint2 *>(&b.v[d][src ^ ((d >> 1) & 7)])[qq & 1];
                     uint32_t h0, h1, h2, h3;
-                    i8x4_to_f16(w8.x, h0, h1);
-                    i8x4_to_f16(w8.y, h2, h3);
+                    i8x8_to_f16_sdwa(w8.x, w8.y, h0, h1, h2, h3);
                     const half8 va8 = __builtin_bit_cast(half8, make_uint4(h0, h1, h2, h3));
                     o[jj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va8, ps, o[jj], 0, 0, 0);
                 }
