@@ -443,6 +443,37 @@ struct DecodeParams {
 
 // sigmoid(x) = 1 / (1 + 2^(-x log2(e))) with the hardware exponential and reciprocal (about an ulp
 // each), as the prefill kernels compute it
+// x of lane l ^ 16 (v_permlane16_swap) and of lane l ^ 32 (v_permlane32_swap) added or maxed in:
+// with both operands holding x, every lane ends with its own value in one register and its
+// partner's in the other; the no-ops cover the cross-lane move's wait states. Registers, not an
+// LDS round trip as a shuffle takes.
+__device__ inline float xl_sum16(float x) {
+    float a = x, b = x;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+    return a + b;
+}
+__device__ inline float xl_sum32(float x) {
+    float a = x, b = x;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+    return a + b;
+}
+__device__ inline float xl_max16(float x) {
+    float a = x, b = x;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+    return fmaxf(a, b);
+}
+__device__ inline float xl_max32(float x) {
+    float a = x, b = x;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+    return fmaxf(a, b);
+}
+// x of lane l ^ 8 (the other half of its 16-lane row) by a DPP rotation of the row by 8
+__device__ inline float xl_swap8(float x) {
+    float y;
+    asm volatile("s_nop 1\n\tv_mov_b32_dpp %0, %1 row_ror:8 row_mask:0xf bank_mask:0xf" : "=v"(y) : "v"(x));
+    return y;
+}
+
 __device__ inline float sigmoidf(float x) {
     return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
 }
@@ -847,8 +878,8 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
             const _Float16 hi = (_Float16)scaled;
             hv[r] = lo_col ? (_Float16)(scaled - (float)hi) : hi;
         }
-        total += __shfl_xor(total, 16, 64);
-        total += __shfl_xor(total, 32, 64);
+        total = xl_sum16(total);
+        total = xl_sum32(total);
         const half4 pop = {hv[0], hv[1], hv[2], hv[3]};
         pshare[slot][wave][lane] = __builtin_bit_cast(uint2, pop);
     };
@@ -931,15 +962,15 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
             float top = -INFINITY;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int mine = acc[r], other = __shfl_xor(mine, 8, 64);
-                const float hi = (float)(lo_col ? other : mine), lo = (float)(lo_col ? mine : other);
+                const float mine = (float)acc[r], other = xl_swap8(mine);   // exact: |dot| < 2^22
+                const float hi = lo_col ? other : mine, lo = lo_col ? mine : other;
                 const float full = fmaf((float)acc3[r], 1.0f / 64516.0f, fmaf(lo, 1.0f / 254.0f, hi)) * qsc;
                 const float value = t0 + r < end ? full * kscale[local0 + r] : -INFINITY;
                 sc_prev[r] = value;
                 top = fmaxf(top, value);
             }
-            top = fmaxf(top, __shfl_xor(top, 16, 64));
-            top = fmaxf(top, __shfl_xor(top, 32, 64));
+            top = xl_max16(top);
+            top = xl_max32(top);
             local_prev = local0;
             probs(sc_prev, local0, m, total_prev, j & 1);
             if (qq == 0) chunk_top[j & 1][wave][n] = top;
