@@ -780,16 +780,15 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
         }
     }
 
-    // ---- scales of the split (this group) into LDS, vs_ref = their maximum; the
-    // per-head maxima of the query chunks
+    // ---- K scales of the split (this group) into LDS, vs_ref = the maximum of its V scales;
+    // the per-head maxima of the query chunks
 #pragma unroll
     for (int it = 0; it < kMaxSplitTokens / 512; it++) {
         const uint32_t e = tid + 512 * it;   // < kMaxSplitTokens; entries past the split are never read
         // entries past the split are zero (selected after the unconditional loads); in append
-        // mode the new token's entry is set from its fresh scales below
+        // mode the new token's entry is set from its fresh scale below
         const bool inside = begin + e < end && (int)e != e_new;
         kscale[e] = inside ? ksv[it] * (kLog2e / 16.0f) : 0.0f;
-        vscale[e] = inside ? vsv[it] : 0.0f;
         vmax = fmaxf(vmax, inside ? vsv[it] : 0.0f);
     }
     if (p.append) {
@@ -799,10 +798,7 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
 #pragma unroll
             for (int f = 0; f < 4; f++) x[f] = *reinterpret_cast<const float4 *>(&qrot0[head][16 * qq + 4 * f]);
         }
-        if (tid == 0 && owner) {
-            kscale[e_new] = fresh_scale[0] * (kLog2e / 16.0f);
-            vscale[e_new] = fresh_scale[1];
-        }
+        if (tid == 0 && owner) kscale[e_new] = fresh_scale[0] * (kLog2e / 16.0f);
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) vmax = fmaxf(vmax, __shfl_xor(vmax, o, 64));
@@ -818,6 +814,14 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
 #pragma unroll
     for (int w = 1; w < kDecodeWaves; w++) vs_ref = fmaxf(vs_ref, red[w]);
     const float vs_inv = vs_ref > 0.0f ? 1.0f / vs_ref : 0.0f;
+    // the split's V scales times 1 / vs_ref, the factor of the probability operand (entries past
+    // the split zero, the new token's from its fresh scale); the barrier before phase 0 publishes them
+#pragma unroll
+    for (int it = 0; it < kMaxSplitTokens / 512; it++) {
+        const uint32_t e = tid + 512 * it;
+        const float s = (int)e == e_new ? fresh_scale[1] : vsv[it];
+        vscale[e] = begin + e < end ? s * vs_inv : 0.0f;
+    }
     // ---- INT8 query operands of chunk c = wave: q ~= s_q (q1 + q2 / 254 + q3 / 254^2).
     // z = q / s_q lies in [-127, 127]; q1 = rint(z) and r1 = z - q1 (exact, |r1| <= 1/2);
     // q2 = rint(254 r1) and r2 = 254 r1 - q2 (one rounding, |r2| <= 1/2 + 2^-17);
@@ -868,13 +872,16 @@ __global__ __launch_bounds__(512, 1) void decode_int8_kernel(DecodeParams p) {
     // n < 8) or lo (n >= 8) part of p * vs / vs_ref, published as this wave's P operand in
     // slot `slot`; total = the column's sum over the wave's 16 tokens.
     auto probs = [&](const float (&sc)[4], int local0, float ref, float &total, int slot) __attribute__((always_inline)) {
+        // ref = -inf (before the first rescale) gives +inf for unmasked tokens: their chunk
+        // always rescales, which rebuilds the operands and the total before either is read
+        const float refc = fmaxf(ref, -3.0e38f);
         _Float16 hv[4];
         total = 0.0f;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const float prob = ref == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sc[r] - ref);   // 0 for masked tokens
+            const float prob = __builtin_amdgcn_exp2f(sc[r] - refc);   // 0 for masked tokens
             total += prob;
-            const float scaled = prob * (vscale[local0 + r] * vs_inv);
+            const float scaled = prob * vscale[local0 + r];
             const _Float16 hi = (_Float16)scaled;
             hv[r] = lo_col ? (_Float16)(scaled - (float)hi) : hi;
         }
